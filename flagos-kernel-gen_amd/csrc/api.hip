@@ -1,0 +1,299 @@
+// C ABI entry points (declared in include/mw4a8.h): argument validation,
+// tile selection, workspace carving and kernel launches. Host code only.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/mw4a8.h"
+#include "mw4a8_internal.h"
+#include "mw4a8_pack.h"
+
+using namespace mw4a8;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(MW4A8_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+bool supported_group(int gs) { return gs == 64 || gs == 128 || gs == 256; }
+
+// Checks shared by the GEMM entries. Returns MW4A8_OK or an error code.
+int check_gemm_args(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
+                    const float* w_scale, const int8_t* w_zero, const void* out, int64_t ldo, int rows,
+                    int N, int K, int E, int gs, bool need_scales) {
+  if (rows < 0 || N <= 0 || K <= 0 || E <= 0)
+    return fail(MW4A8_ERR_INVALID, "bad sizes: rows=%d N=%d K=%d E=%d", rows, N, K, E);
+  if (!supported_group(gs)) return fail(MW4A8_ERR_UNSUPPORTED, "group_size %d not in {64,128,256}", gs);
+  if (K % gs != 0) return fail(MW4A8_ERR_INVALID, "K=%d is not a multiple of group_size=%d", K, gs);
+  if (ldx < K) return fail(MW4A8_ERR_INVALID, "ldx=%lld < K=%d", (long long)ldx, K);
+  if (ldo < N) return fail(MW4A8_ERR_INVALID, "ldo=%lld < N=%d", (long long)ldo, N);
+  if (ldx % 16 != 0) return fail(MW4A8_ERR_INVALID, "ldx=%lld must be a multiple of 16", (long long)ldx);
+  if (!x_q || !w_q4 || !w_zero || !out || (need_scales && (!x_scale || !w_scale)))
+    return fail(MW4A8_ERR_INVALID, "null tensor pointer");
+  if (!aligned(x_q, 16) || !aligned(w_q4, 16))
+    return fail(MW4A8_ERR_INVALID, "x_q and w_q4 must be 16-byte aligned");
+  if ((need_scales && (!aligned(x_scale, 4) || !aligned(w_scale, 4))) || !aligned(out, 2))
+    return fail(MW4A8_ERR_INVALID, "misaligned scale or output pointer");
+  return MW4A8_OK;
+}
+
+struct CsrWorkspace {
+  int32_t* count;
+  int32_t* expert;
+  int32_t* row0;
+  int32_t* row1;
+};
+
+size_t csr_ws_bytes(int max_blocks) {
+  const size_t b = 256 + 3 * sizeof(int32_t) * (size_t)max_blocks;
+  return (b + 255) & ~(size_t)255;
+}
+
+CsrWorkspace carve(void* ws, int max_blocks) {
+  char* p = static_cast<char*>(ws);
+  CsrWorkspace w;
+  w.count = reinterpret_cast<int32_t*>(p);
+  w.expert = reinterpret_cast<int32_t*>(p + 256);
+  w.row0 = w.expert + max_blocks;
+  w.row1 = w.row0 + max_blocks;
+  return w;
+}
+
+GemmArgs base_args(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
+                   const float* w_scale, const int8_t* w_zero, uint16_t* out, int64_t ldo, int N, int K,
+                   int gs) {
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = x_q;
+  a.ldx = ldx;
+  a.xs = x_scale;
+  a.w = w_q4;
+  a.ws = w_scale;
+  a.wz = w_zero;
+  a.out = out;
+  a.ldo = ldo;
+  a.N = N;
+  a.K = K;
+  a.G = K / gs;
+  return a;
+}
+
+// Shared by the reference-layout GEMM and the debug export: build the block
+// table on the device, then launch.
+int run_csr(GemmArgs a, const int32_t* offsets, int M_total, int E, int gs, void* workspace, size_t ws_bytes,
+            hipStream_t s, bool debug) {
+  if (!offsets) return fail(MW4A8_ERR_INVALID, "null expert_offsets");
+  const int ne = E < M_total ? E : M_total;
+  TileConfig cfg = debug ? TileConfig{16, 16, 4, 512 / gs, 1} : select_tiles(M_total, ne, a.N, a.K, gs);
+  const int max_blocks = max_row_blocks(M_total, E, cfg.BM);
+  if (max_blocks == 0) return MW4A8_OK;
+  if (!workspace || ws_bytes < csr_ws_bytes(max_blocks))
+    return fail(MW4A8_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", csr_ws_bytes(max_blocks),
+                workspace ? ws_bytes : (size_t)0);
+  if (!aligned(workspace, 256)) return fail(MW4A8_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  CsrWorkspace w = carve(workspace, max_blocks);
+  hipError_t e = launch_csr_block_table(offsets, E, M_total, cfg.BM, max_blocks, w.expert, w.row0, w.row1,
+                                        w.count, s);
+  if (e != hipSuccess) return hip_fail(e, "block table launch");
+  a.blk_expert = w.expert;
+  a.blk_row0 = w.row0;
+  a.blk_row1 = w.row1;
+  a.blk_count = w.count;
+  e = debug ? launch_debug_partials(a, gs, max_blocks, s) : launch_grouped_gemm(a, cfg, gs, false, max_blocks, s);
+  if (e != hipSuccess) return hip_fail(e, "grouped GEMM launch");
+  return MW4A8_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mw4a8_last_error(void) { return g_err; }
+
+int mw4a8_abi_version(void) { return 1; }
+
+size_t mw4a8_workspace_bytes(int M_total, int N, int K, int E, int group_size) {
+  (void)N;
+  (void)K;
+  (void)group_size;
+  if (M_total <= 0 || E <= 0) return 256;
+  return csr_ws_bytes(max_row_blocks(M_total, E, 16));
+}
+
+int mw4a8_grouped_gemm(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
+                       const float* w_scale, const int8_t* w_zero, const int32_t* expert_offsets,
+                       uint16_t* out_bf16, int64_t ldo, int M_total, int N, int K, int E, int group_size,
+                       void* workspace, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  if (M_total == 0) return MW4A8_OK;
+  int rc = check_gemm_args(x_q, ldx, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, M_total, N, K, E,
+                           group_size, true);
+  if (rc) return rc;
+  GemmArgs a = base_args(x_q, ldx, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, N, K, group_size);
+  return run_csr(a, expert_offsets, M_total, E, group_size, workspace, ws_bytes,
+                 static_cast<hipStream_t>(stream), false);
+}
+
+int mw4a8_debug_partials(const int8_t* x_q, int64_t ldx, const uint8_t* w_q4, const int8_t* w_zero,
+                         const int32_t* expert_offsets, int32_t* partials, int M_total, int N, int K,
+                         int E, int group_size, void* workspace, size_t ws_bytes, void* stream) {
+  g_err[0] = 0;
+  if (M_total == 0) return MW4A8_OK;
+  int rc = check_gemm_args(x_q, ldx, nullptr, w_q4, nullptr, w_zero, partials, N, M_total, N, K, E,
+                           group_size, false);
+  if (rc) return rc;
+  GemmArgs a = base_args(x_q, ldx, nullptr, w_q4, nullptr, w_zero, nullptr, N, N, K, group_size);
+  a.dbg = partials;
+  return run_csr(a, expert_offsets, M_total, E, group_size, workspace, ws_bytes,
+                 static_cast<hipStream_t>(stream), true);
+}
+
+int mw4a8_align_sizes(int num_pairs, int E, int block_m, int* sorted_len, int* blocks_len) {
+  g_err[0] = 0;
+  if (num_pairs < 0 || E <= 0 || block_m <= 0 || !sorted_len || !blocks_len)
+    return fail(MW4A8_ERR_INVALID, "bad align sizes arguments");
+  const int64_t sl = (int64_t)num_pairs + (int64_t)E * (block_m - 1);
+  if (sl > 0x7fffffff) return fail(MW4A8_ERR_UNSUPPORTED, "routing buffer too large");
+  *sorted_len = (int)sl;
+  *blocks_len = (int)((sl + block_m - 1) / block_m);
+  return MW4A8_OK;
+}
+
+int mw4a8_select_block_m(int num_pairs, int E, int N, int K, int group_size) {
+  const int ne = E < num_pairs ? E : num_pairs;
+  return select_tiles(num_pairs, ne, N, K, group_size).BM;
+}
+
+int mw4a8_moe_align(const int32_t* topk_ids, int num_pairs, int E, int block_m, int32_t* sorted_ids,
+                    int32_t* expert_ids, int32_t* num_post_pad, int32_t* expert_offsets_out, void* stream) {
+  g_err[0] = 0;
+  if (num_pairs < 0 || E <= 0 || block_m <= 0) return fail(MW4A8_ERR_INVALID, "bad routing sizes");
+  if (E > 1024) return fail(MW4A8_ERR_UNSUPPORTED, "E=%d > 1024 experts", E);
+  if ((num_pairs > 0 && !topk_ids) || !sorted_ids || !expert_ids || !num_post_pad)
+    return fail(MW4A8_ERR_INVALID, "null routing pointer");
+  int sorted_len, blocks_len;
+  int rc = mw4a8_align_sizes(num_pairs, E, block_m, &sorted_len, &blocks_len);
+  if (rc) return rc;
+  hipError_t e = launch_moe_align(topk_ids, num_pairs, E, block_m, sorted_ids, sorted_len, expert_ids,
+                                  blocks_len, num_post_pad, expert_offsets_out, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "moe_align launch");
+  return MW4A8_OK;
+}
+
+int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
+                    const float* w_scale, const int8_t* w_zero, const int32_t* sorted_ids,
+                    const int32_t* expert_ids, const int32_t* num_post_pad, const float* topk_weights,
+                    int topk, uint16_t* out_bf16, int64_t ldo, int M, int N, int K, int E, int group_size,
+                    int block_m, void* stream) {
+  g_err[0] = 0;
+  if (topk <= 0) return fail(MW4A8_ERR_INVALID, "topk=%d", topk);
+  if (M == 0) return MW4A8_OK;
+  int rc = check_gemm_args(x_q, ldx, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, M, N, K, E, group_size,
+                           true);
+  if (rc) return rc;
+  if (!sorted_ids || !expert_ids || !num_post_pad || !topk_weights)
+    return fail(MW4A8_ERR_INVALID, "null routing pointer");
+  if (!aligned(topk_weights, 4)) return fail(MW4A8_ERR_INVALID, "misaligned topk_weights");
+  if (block_m != 16 && block_m != 32 && block_m != 64 && block_m != 128)
+    return fail(MW4A8_ERR_UNSUPPORTED, "block_m=%d not in {16,32,64,128}", block_m);
+  const int64_t pairs = (int64_t)M * topk;
+  if (pairs > 0x7fffffff / 2) return fail(MW4A8_ERR_UNSUPPORTED, "too many pairs");
+  GemmArgs a = base_args(x_q, ldx, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, N, K, group_size);
+  a.sorted_ids = sorted_ids;
+  a.expert_ids = expert_ids;
+  a.num_post_pad = num_post_pad;
+  a.tw = topk_weights;
+  a.topk = topk;
+  a.num_pairs = (int)pairs;
+  a.E = E;
+  int sorted_len, blocks_len;
+  rc = mw4a8_align_sizes((int)pairs, E, block_m, &sorted_len, &blocks_len);
+  if (rc) return rc;
+  a.sorted_len = sorted_len;
+  const int ne = E < (int)pairs ? E : (int)pairs;
+  TileConfig cfg = select_tiles((int)pairs, ne, N, K, group_size);
+  // the routing metadata fixes the row block; keep the rest of the choice
+  if (cfg.BM != block_m) {
+    const TileConfig forced = select_tiles(block_m * ne, ne, N, K, group_size);
+    cfg = forced;
+  }
+  const int max_blocks = max_row_blocks((int)pairs, E, block_m);
+  hipError_t e = launch_grouped_gemm(a, cfg, group_size, true, max_blocks, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "fused MoE launch");
+  return MW4A8_OK;
+}
+
+// ---------------------------------------------------------------------------
+
+int mw4a8_host_selftest(void) {
+  int bad = 0;
+  // zero fold: every nibble against every zero point, in every byte lane
+  for (int z = -128; z <= 127; ++z) {
+    const ZeroFold f = make_zero_fold(z);
+    for (int u = 0; u < 16; ++u) {
+      const int8_t want = (int8_t)(uint8_t)((u - z) & 0xff);
+      for (int lane = 0; lane < 4; ++lane) {
+        const uint32_t lo_word = (uint32_t)u << (8 * lane);         // nibble in the low half of byte `lane`
+        const uint32_t hi_word = (uint32_t)(u << 4) << (8 * lane);  // nibble in the high half
+        const int8_t got_lo = (int8_t)((fold_even(lo_word, f) >> (8 * lane)) & 0xff);
+        const int8_t got_hi = (int8_t)((fold_odd(hi_word, f) >> (8 * lane)) & 0xff);
+        bad += got_lo != want;
+        bad += got_hi != want;
+      }
+    }
+  }
+  // K relabelling: one lane's 16-k dot product computed from the relabelled
+  // activation bytes and the unpacked weight words equals the natural-order dot
+  uint32_t state = 12345u;
+  auto rnd = [&state]() {
+    state = state * 1664525u + 1013904223u;
+    return state >> 8;
+  };
+  for (int trial = 0; trial < 2000; ++trial) {
+    int8_t x[16];
+    uint8_t packed[8];
+    for (int i = 0; i < 16; ++i) x[i] = (int8_t)(rnd() & 0xff);
+    for (int i = 0; i < 8; ++i) packed[i] = (uint8_t)(rnd() & 0xff);
+    const int z = (int)(rnd() % 256) - 128;
+    int64_t want = 0;
+    for (int k = 0; k < 16; ++k) {
+      const int u = (k & 1) ? (packed[k / 2] >> 4) : (packed[k / 2] & 15);
+      want += (int64_t)x[k] * (int8_t)(uint8_t)((u - z) & 0xff);
+    }
+    uint32_t xd[4], pd[2];
+    memcpy(xd, x, 16);
+    memcpy(pd, packed, 8);
+    const uint32_t a[4] = {even_bytes(xd[0], xd[1]), odd_bytes(xd[0], xd[1]), even_bytes(xd[2], xd[3]),
+                           odd_bytes(xd[2], xd[3])};
+    const ZeroFold f = make_zero_fold(z);
+    const uint32_t bw[4] = {fold_even(pd[0], f), fold_odd(pd[0], f), fold_even(pd[1], f), fold_odd(pd[1], f)};
+    int64_t got = 0;
+    for (int w = 0; w < 4; ++w)
+      for (int by = 0; by < 4; ++by)
+        got += (int64_t)(int8_t)((a[w] >> (8 * by)) & 0xff) * (int8_t)((bw[w] >> (8 * by)) & 0xff);
+    bad += got != want;
+  }
+  // bf16 round to nearest even
+  struct Case { uint32_t in; uint16_t out; };
+  const Case cases[] = {
+      {0x3f800000u, 0x3f80}, {0x3f808000u, 0x3f80}, {0x3f818000u, 0x3f82}, {0x3f808001u, 0x3f81},
+      {0xbf80ffffu, 0xbf81}, {0x7f7fffffu, 0x7f80}, {0x00000000u, 0x0000}, {0x7fc00000u, 0x7fc0}};
+  for (const Case& c : cases) bad += bf16_rne_bits(c.in) != c.out;
+  if (bad) fail(MW4A8_ERR_INVALID, "host self-test: %d checks failed", bad);
+  return bad;
+}
+
+}  // extern "C"

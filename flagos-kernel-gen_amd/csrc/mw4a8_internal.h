@@ -1,0 +1,70 @@
+// Internal interfaces between the C-ABI layer (api.cpp) and the HIP kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mw4a8 {
+
+// Everything a grouped-GEMM launch needs. Exactly one of the two row
+// sources is used: the CSR block table (reference layout, rows grouped by
+// expert) or the routing metadata (routed layout, rows gathered per pair).
+struct GemmArgs {
+  const int8_t* x;        // [rows, K] int8, row stride ldx bytes
+  int64_t ldx;
+  const float* xs;        // per-row activation scale
+  const uint8_t* w;       // [E, N, K/2] packed int4
+  const float* ws;        // [E, N, G] group scales
+  const int8_t* wz;       // [E, N, G] zero points
+  // reference layout: block b covers rows [row0[b], row1[b]) of expert blk_expert[b]
+  const int32_t* blk_expert;
+  const int32_t* blk_row0;
+  const int32_t* blk_row1;
+  const int32_t* blk_count;   // [0] = number of valid blocks
+  // routed layout: block b covers sorted slots [b*BM, b*BM+BM)
+  const int32_t* sorted_ids;
+  const int32_t* expert_ids;
+  const int32_t* num_post_pad;
+  const float* tw;            // [num_pairs] routing weights
+  int topk;
+  int num_pairs;
+  int sorted_len;             // length of sorted_ids (reads are bounded by it)
+  int E;
+  uint16_t* out;              // bf16 bits, row stride ldo elements
+  int64_t ldo;
+  int32_t* dbg;               // debug partials [rows, N, G] (debug kernels only)
+  int N, K, G;
+  // launch geometry (see grid_for)
+  int n_tiles, R, total_tiles, per_xcd;
+};
+
+struct TileConfig {
+  int BM;     // rows per block
+  int WN;     // columns per wave
+  int NW;     // waves per workgroup
+  int KCG;    // K-groups staged per chunk
+  int R;      // row blocks walked together per column tile (L2 reuse)
+};
+
+// Tile choice by expected rows per touched expert (no device sync).
+TileConfig select_tiles(int rows, int touched_experts, int N, int K, int group_size);
+
+// Upper bound on the number of row blocks for `rows` rows spread over at
+// most `experts` experts: every expert adds at most one partial block.
+int max_row_blocks(int rows, int experts, int BM);
+
+// Kernel launchers; return hipSuccess or the launch error.
+hipError_t launch_csr_block_table(const int32_t* offsets, int E, int M_total, int BM, int max_blocks,
+                                  int32_t* blk_expert, int32_t* blk_row0, int32_t* blk_row1,
+                                  int32_t* blk_count, hipStream_t s);
+
+hipError_t launch_moe_align(const int32_t* topk_ids, int num_pairs, int E, int BM,
+                            int32_t* sorted_ids, int sorted_len, int32_t* expert_ids, int blocks_len,
+                            int32_t* num_post_pad, int32_t* expert_offsets, hipStream_t s);
+
+// max_blocks bounds the row-block index space the grid covers.
+hipError_t launch_grouped_gemm(GemmArgs a, const TileConfig& cfg, int group_size, bool routed,
+                               int max_blocks, hipStream_t s);
+
+hipError_t launch_debug_partials(GemmArgs a, int group_size, int max_blocks, hipStream_t s);
+
+}  // namespace mw4a8

@@ -1,0 +1,145 @@
+/*
+ * mw4a8.h -- C ABI of the MI355X (gfx950) W4A8 fused-MoE grouped GEMM.
+ *
+ * Library: flagos-kernel-gen_amd/libmw4a8.so (built by
+ * flagos-kernel-gen_amd/build.py with hipcc for gfx950).
+ *
+ * Conventions shared by every entry point:
+ *  - All array arguments are device pointers (HIP device memory) owned by
+ *    the caller. The library allocates nothing, never synchronises the host
+ *    and keeps no mutable global state; calls on different streams may run
+ *    concurrently.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *    Work is only enqueued; results are valid once the stream reaches it.
+ *  - Return value: MW4A8_OK (0) or a negative MW4A8_ERR_* code; the message
+ *    of the last failure on the calling thread is mw4a8_last_error().
+ *  - bf16 values are passed as their raw 16-bit patterns (uint16_t).
+ *
+ * Reference interface: the Python operator
+ *   w4a8_group_gemm_moe(x_q, x_scale, w_q4_packed, w_scale, w_zero,
+ *                       expert_offsets, out, group_size) -> out
+ * (reference docs/Task1.md:8-17, implemented on GPU at
+ *  Task1/v1.6/task1-codex5.5-all-v1.6.py:986-1030, which an external harness
+ *  looks up by name, docs/提交要求.md:3).
+ */
+#ifndef MW4A8_H
+#define MW4A8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MW4A8_OK 0
+#define MW4A8_ERR_INVALID (-1)      /* bad argument: null pointer, shape, stride, alignment */
+#define MW4A8_ERR_UNSUPPORTED (-2)  /* valid but unsupported: group size, block_m, E > 1024 */
+#define MW4A8_ERR_WORKSPACE (-3)    /* workspace missing or smaller than mw4a8_workspace_bytes */
+#define MW4A8_ERR_HIP (-4)          /* a HIP launch failed */
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* mw4a8_last_error(void);
+
+/* ABI version of this header (increments on incompatible changes). */
+int mw4a8_abi_version(void);
+
+/*
+ * Bytes of device workspace mw4a8_grouped_gemm / mw4a8_debug_partials need
+ * for this problem (a per-call block table; 256-byte aligned size).
+ */
+size_t mw4a8_workspace_bytes(int M_total, int N, int K, int E, int group_size);
+
+/*
+ * Reference-layout grouped GEMM. Replaces the whole reference operator
+ * (docs/Task1.md:53-114; GPU launch path
+ * Task1/v1.6/task1-codex5.5-all-v1.6.py:656-710):
+ *   for every expert e and row m in [offsets[e], offsets[e+1]):
+ *     out[m, n] = bf16( x_scale[m] * sum_g w_scale[e,n,g] *
+ *                 sum_{k in g} x_q[m,k] * int8(nib(w_q4[e,n,k/2], k) - w_zero[e,n,g]) )
+ *  x_q      [M_total, K] int8, row stride ldx bytes (multiple of 16, ptr 16-byte aligned)
+ *  x_scale  [M_total] fp32
+ *  w_q4     [E, N, K/2] uint8, contiguous; low nibble = even k
+ *  w_scale  [E, N, K/group_size] fp32, contiguous
+ *  w_zero   [E, N, K/group_size] int8, contiguous
+ *  expert_offsets [E+1] int32 (CSR; ranges are clamped to [0, M_total])
+ *  out      [M_total, N] bf16, row stride ldo elements; rows owned by no
+ *           expert are left untouched (docs/Task1.md:91-92)
+ *  group_size in {64, 128, 256}; K a multiple of group_size.
+ * Offsets are read on the device; no host synchronisation.
+ */
+int mw4a8_grouped_gemm(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
+                       const float* w_scale, const int8_t* w_zero, const int32_t* expert_offsets,
+                       uint16_t* out_bf16, int64_t ldo, int M_total, int N, int K, int E, int group_size,
+                       void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Lengths of the routing buffers for num_pairs = M * topk pairs:
+ *  *sorted_len = num_pairs + E * (block_m - 1), *blocks_len = ceil(sorted_len / block_m).
+ * No reference counterpart (the reference receives pre-grouped rows).
+ */
+int mw4a8_align_sizes(int num_pairs, int E, int block_m, int* sorted_len, int* blocks_len);
+
+/*
+ * Row-block size the library would pick for a routed problem (16, 32, 64
+ * or 128), chosen from the expected rows per touched expert. Mirrors the
+ * reference's block-M heuristic (Task1/v1.6/task1-codex5.5-all-v1.6.py:648-653)
+ * without its device->host read of the per-expert maximum (:62-64).
+ */
+int mw4a8_select_block_m(int num_pairs, int E, int N, int K, int group_size);
+
+/*
+ * moe_align_block_size-style routing metadata for topk_ids [num_pairs]
+ * (pairs i = m * topk + j). No reference counterpart; with block_m = 1 the
+ * unpadded offsets equal the reference's expert_offsets for rows laid out
+ * in sorted order (docs/Task1.md:87-92).
+ *  sorted_ids  [sorted_len]  slot block_off[e]*block_m + r holds the r-th pair
+ *                            of expert e (ascending); other slots = num_pairs
+ *  expert_ids  [blocks_len]  owner of each block, -1 past the last block
+ *  num_post_pad [1]          block_off[E] * block_m
+ *  expert_offsets_out [E+1]  exclusive prefix of per-expert pair counts (may be NULL)
+ * Ids outside [0, E) are not routed. E <= 1024.
+ */
+int mw4a8_moe_align(const int32_t* topk_ids, int num_pairs, int E, int block_m, int32_t* sorted_ids,
+                    int32_t* expert_ids, int32_t* num_post_pad, int32_t* expert_offsets_out, void* stream);
+
+/*
+ * Routed grouped GEMM with the top-k weight epilogue. No reference
+ * counterpart; per pair i = m * topk + j routed to expert e:
+ *   out[i, n] = bf16( (acc_e(x_q[m])[n] * x_scale[m]) * topk_weights[i] )
+ * where acc_e is the reference reduction of docs/Task1.md:99-107.
+ *  x_q [M, K] int8 (stride ldx), x_scale [M], topk_weights [M * topk] fp32,
+ *  sorted_ids / expert_ids / num_post_pad from mw4a8_moe_align with the
+ *  same block_m, out [M * topk, N] bf16 (stride ldo). Rows of pairs that are
+ *  not routed are left untouched. block_m in {16, 32, 64, 128}.
+ */
+int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
+                    const float* w_scale, const int8_t* w_zero, const int32_t* sorted_ids,
+                    const int32_t* expert_ids, const int32_t* num_post_pad, const float* topk_weights,
+                    int topk, uint16_t* out_bf16, int64_t ldo, int M, int N, int K, int E, int group_size,
+                    int block_m, void* stream);
+
+/*
+ * Debug export of the exact int32 per-group partial sums
+ *   partials[m, n, g] = sum_{k in g} x_q[m,k] * int8(nib - zero)
+ * (reference docs/Task1.md:99-104, the "mgk,ngk->mng" einsum) for the
+ * rows owned by some expert; other rows are left untouched.
+ * partials: [M_total, N, K/group_size] int32. Workspace as mw4a8_grouped_gemm.
+ */
+int mw4a8_debug_partials(const int8_t* x_q, int64_t ldx, const uint8_t* w_q4, const int8_t* w_zero,
+                         const int32_t* expert_offsets, int32_t* partials, int M_total, int N, int K,
+                         int E, int group_size, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * CPU-only self-test of the operand packing helpers the kernels use
+ * (zero-point fold over all 16 x 256 nibble/zero pairs, the K relabelling
+ * of activations vs weights, bf16 rounding). Returns 0 on success, else the
+ * number of failed checks. Needs no GPU.
+ */
+int mw4a8_host_selftest(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MW4A8_H */
