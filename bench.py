@@ -215,6 +215,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--headline-only", action="store_true")
+    ap.add_argument("--workload", default=None,
+                    help="name:M to measure instead of the headline (profiling); implies --headline-only")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -226,8 +228,12 @@ def main():
     pkg = __graft_entry__.import_package()
     dev = torch.device("cuda:0")
 
-    log(f"headline {HEADLINE[0]} M={HEADLINE[1]}")
-    hp = Point(pkg, HEADLINE[0], HEADLINE[1], dev)
+    head_name, head_m = HEADLINE
+    if args.workload:
+        head_name, head_m = args.workload.split(":")[0], int(args.workload.split(":")[1])
+        args.headline_only = True
+    log(f"headline {head_name} M={head_m}")
+    hp = Point(pkg, head_name, head_m, dev)
     head = measure_point(hp, args.steps, args.warmup)
     log(json.dumps(head))
     del hp

@@ -6,7 +6,8 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmw4a8.so")
+# MW4A8_LIB may point at another build of the same C ABI (e.g. an experimental one)
+LIB_PATH = os.environ.get("MW4A8_LIB") or os.path.join(HERE, "libmw4a8.so")
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int

@@ -47,6 +47,10 @@ int check_gemm_args(const int8_t* x_q, int64_t ldx, const float* x_scale, const 
     return fail(MW4A8_ERR_INVALID, "x_q and w_q4 must be 16-byte aligned");
   if ((need_scales && (!aligned(x_scale, 4) || !aligned(w_scale, 4))) || !aligned(out, 2))
     return fail(MW4A8_ERR_INVALID, "misaligned scale or output pointer");
+  // kernels address each tensor (weights: one expert's slice) with 32-bit offsets
+  const int64_t lim = (int64_t)1 << 31;
+  if ((int64_t)rows * ldx >= lim || (int64_t)N * (K / 2) >= lim || (int64_t)N * (K / gs) * 4 >= lim)
+    return fail(MW4A8_ERR_UNSUPPORTED, "tensor too large for 32-bit offsets (rows*ldx, N*K/2, N*G*4 < 2^31)");
   return MW4A8_OK;
 }
 
@@ -143,6 +147,7 @@ int mw4a8_grouped_gemm(const int8_t* x_q, int64_t ldx, const float* x_scale, con
                            group_size, true);
   if (rc) return rc;
   GemmArgs a = base_args(x_q, ldx, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, N, K, group_size);
+  a.x_bytes = (uint32_t)(M_total * ldx);
   return run_csr(a, expert_offsets, M_total, E, group_size, workspace, ws_bytes,
                  static_cast<hipStream_t>(stream), false);
 }
@@ -157,6 +162,7 @@ int mw4a8_debug_partials(const int8_t* x_q, int64_t ldx, const uint8_t* w_q4, co
   if (rc) return rc;
   GemmArgs a = base_args(x_q, ldx, nullptr, w_q4, nullptr, w_zero, nullptr, N, N, K, group_size);
   a.dbg = partials;
+  a.x_bytes = (uint32_t)(M_total * ldx);
   return run_csr(a, expert_offsets, M_total, E, group_size, workspace, ws_bytes,
                  static_cast<hipStream_t>(stream), true);
 }
@@ -212,6 +218,7 @@ int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const 
   const int64_t pairs = (int64_t)M * topk;
   if (pairs > 0x7fffffff / 2) return fail(MW4A8_ERR_UNSUPPORTED, "too many pairs");
   GemmArgs a = base_args(x_q, ldx, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, N, K, group_size);
+  a.x_bytes = (uint32_t)(M * ldx);
   a.sorted_ids = sorted_ids;
   a.expert_ids = expert_ids;
   a.num_post_pad = num_post_pad;

@@ -4,20 +4,28 @@
 // split the BN columns (WN columns each) and all share the BM activation
 // rows, which are staged through LDS once per K-chunk. Each wave streams its
 // own packed int4 weight columns straight from HBM into registers with
-// 128-bit loads (four lanes cover the 64 contiguous bytes of one column's
-// 128-wide K-group), unpacks them to int8 with the zero point folded in
-// (mw4a8_pack.h), and feeds v_mfma_i32_16x16x64_i8.
+// 128-bit buffer loads (four lanes cover the 64 contiguous bytes of one
+// column's 128-wide K-group), unpacks them to int8 with the zero point folded
+// in (mw4a8_pack.h), and feeds v_mfma_i32_16x16x64_i8.
 //
-// Per K-group the int32 MFMA accumulators start from zero; at the end of the
-// group they are converted to fp32 and multiplied by the group scale into an
-// fp32 accumulator (docs/Task1.md:99-107, int32 per group as the Hygon
-// kernel does it). The epilogue multiplies by the per-row activation scale
-// and, for routed launches, the top-k routing weight, rounds to bf16 and
-// stores the row (docs/Task1.md:109-112).
+// Per K-group and 16-row block the int32 MFMA results start from zero; right
+// after the block's MFMAs they are converted to fp32 and multiplied by the
+// group scale into the fp32 accumulator (docs/Task1.md:99-107, int32 per
+// group as the reference's Hygon kernel does it). The epilogue multiplies by
+// the per-row activation scale and, for routed launches, the top-k routing
+// weight, rounds to bf16 and stores the row (docs/Task1.md:109-112).
 //
-// Pipelining: the activation chunk and the weight registers of chunk c+1
-// are requested before chunk c is computed; LDS is double-buffered so one
-// barrier per chunk suffices.
+// Memory access is branch-free: every global read is a raw buffer load whose
+// descriptor covers exactly the tensor (or one expert's slice of it), and
+// lanes with nothing to read (padding rows, columns past N) use an offset
+// beyond the descriptor, which the hardware returns as zero. A tile whose
+// valid rows fit in its top half runs a half-height body, so a nearly empty
+// last row block of an expert costs at most half a tile of MFMAs.
+//
+// Pipelining: the activation chunk and the weight registers of chunk c+1 are
+// requested before chunk c is computed. Weights ping-pong between two
+// register sets (the loop is unrolled by two chunks, so no copies), and LDS
+// is double-buffered, so one barrier per chunk suffices.
 //
 // Grid: a 1-D list of (row block, column tile) pairs, a multiple of 8 long.
 // Workgroup L runs on XCD L % 8, so tile t = (L % 8) * per_xcd + L / 8 gives
@@ -34,31 +42,313 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-template <int BM, int WN, int NW, int GS, int KCG, bool ROUTED, bool DEBUGP>
-__global__ __launch_bounds__(NW * 64) void w4a8_gemm_kernel(const GemmArgs a) {
+constexpr uint32_t kOOB = 0x80000000u;   // buffer offset that reads as zero
+constexpr int kRsrcFlags = 0x00020000;   // raw buffer, 32-bit data format
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcFlags);
+}
+
+// KCG consecutive int8 zero points at byte offset `off` (KCG-aligned) into
+// dst[g * stride + idx], sign-extended.
+template <int KCG, int NB>
+__device__ __forceinline__ void load_zero_run(__amdgpu_buffer_rsrc_t r, uint32_t off, int (&dst)[KCG][NB], int nb) {
+  uint32_t w[(KCG + 3) / 4];
+  if constexpr (KCG == 1) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+  } else if constexpr (KCG == 2) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  } else if constexpr (KCG == 4) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  } else if constexpr (KCG == 8) {
+    const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    w[0] = q.x;
+    w[1] = q.y;
+  } else {
+    static_assert(KCG % 16 == 0, "zero-point run length");
+#pragma unroll
+    for (int h = 0; h < KCG / 16; ++h) {
+      const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * h, 0, 0);
+      w[4 * h] = q.x;
+      w[4 * h + 1] = q.y;
+      w[4 * h + 2] = q.z;
+      w[4 * h + 3] = q.w;
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < KCG; ++g) dst[g][nb] = (int)(int8_t)((w[g / 4] >> (8 * (g % 4))) & 0xffu);
+}
+
+// KCG consecutive fp32 scales at byte offset `off` (4*KCG-aligned up to 16).
+template <int KCG, int NB>
+__device__ __forceinline__ void load_scale_run(__amdgpu_buffer_rsrc_t r, uint32_t off, float (&dst)[KCG][NB],
+                                               int nb) {
+  if constexpr (KCG == 1) {
+    dst[0][nb] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  } else if constexpr (KCG == 2) {
+    const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    dst[0][nb] = __uint_as_float(q.x);
+    dst[1][nb] = __uint_as_float(q.y);
+  } else {
+    static_assert(KCG % 4 == 0, "scale run length");
+#pragma unroll
+    for (int h = 0; h < KCG / 4; ++h) {
+      const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * h, 0, 0);
+      dst[4 * h][nb] = __uint_as_float(q.x);
+      dst[4 * h + 1][nb] = __uint_as_float(q.y);
+      dst[4 * h + 2][nb] = __uint_as_float(q.z);
+      dst[4 * h + 3][nb] = __uint_as_float(q.w);
+    }
+  }
+}
+
+// Per-tile values shared by the kernel's setup and its tile bodies.
+struct TileCtx {
+  int e;          // expert
+  int col0;       // first column of this wave
+  int nchunks;    // K-chunks
+};
+
+// Main K loop and epilogue for the first BMX rows of a tile (BMX <= BM).
+template <int BMX, int BM, int WN, int NW, int GS, int KCG, bool ROUTED, bool DEBUGP>
+__device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, int8_t* s_x, const int* s_src,
+                                          const int* s_dst, const float* s_xs, const float* s_tw) {
   constexpr int NT = NW * 64;
-  constexpr int MB = BM / 16;         // 16-row blocks per tile
+  constexpr int MB = BMX / 16;        // 16-row blocks computed
   constexpr int NB = WN / 16;         // 16-column blocks per wave
-  constexpr int BN = NW * WN;
   constexpr int S = GS / 64;          // MFMA K-steps per group
   constexpr int WD = 2 * S;           // packed dwords per lane per (group, column block)
   constexpr int KC = KCG * GS;        // activation bytes per row per chunk
   constexpr int PITCH = KC + 16;      // LDS row pitch in bytes
+  constexpr int BUF = BM * PITCH;     // bytes per LDS buffer
   constexpr int UPR = KC / 16;        // 16-byte units per row and chunk
-  constexpr int XU = (BM * UPR + NT - 1) / NT;
+  constexpr int XU = (BMX * UPR) / NT;
+  static_assert((BMX * UPR) % NT == 0, "activation chunk must split evenly over the workgroup");
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int jl = lane & 15;   // row (A) / column (B) within a 16-block
+  const int kb = lane >> 4;   // K slot group of the MFMA operands
+  const uint32_t khalf = (uint32_t)a.K / 2;
+
+  // ---- buffer descriptors (one expert's slice for the weights) ------------
+  const int64_t expert_cols = (int64_t)c.e * a.N;
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w + expert_cols * khalf, (uint32_t)a.N * khalf);
+  const __amdgpu_buffer_rsrc_t z_rsrc = make_rsrc(a.wz + expert_cols * a.G, (uint32_t)(a.N * a.G));
+  const __amdgpu_buffer_rsrc_t s_rsrc =
+      make_rsrc(DEBUGP ? (const void*)a.wz : (const void*)(a.ws + expert_cols * a.G),
+                DEBUGP ? 0u : (uint32_t)(a.N * a.G) * 4u);
+  const __amdgpu_buffer_rsrc_t x_rsrc = make_rsrc(a.x, a.x_bytes);
+
+  // per-lane offsets of this lane's weight columns and activation units
+  uint32_t w_off[NB], zs_off[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int col = c.col0 + nb * 16 + jl;
+    const bool ok = col < a.N;
+    w_off[nb] = ok ? (uint32_t)col * khalf + (uint32_t)(kb * (GS / 8)) : kOOB;
+    zs_off[nb] = ok ? (uint32_t)(col * a.G) : kOOB;
+  }
+  uint32_t x_off[XU];
+#pragma unroll
+  for (int j = 0; j < XU; ++j) {
+    const int u = tid + j * NT;
+    const int row = u / UPR;
+    const int src = s_src[row];
+    x_off[j] = src >= 0 ? (uint32_t)(src * a.ldx) + (uint32_t)((u - row * UPR) * 16) : kOOB;
+  }
+
+  // ---- chunk loaders -----------------------------------------------------
+  u32x4 xr[XU];
+  auto load_x = [&](int ch) {
+#pragma unroll
+    for (int j = 0; j < XU; ++j)
+      xr[j] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, x_off[j] + (uint32_t)(ch * KC), 0, 0);
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < XU; ++j) {
+      const int u = tid + j * NT;
+      const int row = u / UPR;
+      const int cu = u - row * UPR;
+      const u32x4 v = xr[j];
+      u32x4 p;
+      p.x = even_bytes(v.x, v.y);
+      p.y = odd_bytes(v.x, v.y);
+      p.z = even_bytes(v.z, v.w);
+      p.w = odd_bytes(v.z, v.w);
+      *reinterpret_cast<u32x4*>(s_x + buf * BUF + row * PITCH + cu * 16) = p;
+    }
+  };
+
+  struct WChunk {
+    uint32_t w[KCG][NB][WD];
+    int z[KCG][NB];
+    float s[KCG][NB];
+  };
+  auto load_w = [&](int ch, WChunk& d) {
+#pragma unroll
+    for (int g = 0; g < KCG; ++g) {
+      const uint32_t gg = (uint32_t)(ch * KCG + g);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint32_t off = w_off[nb] + gg * (GS / 2);
+        if constexpr (S == 1) {
+          const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(w_rsrc, off, 0, 0);
+          d.w[g][nb][0] = q.x;
+          d.w[g][nb][1] = q.y;
+        } else {
+#pragma unroll
+          for (int h = 0; h < S / 2; ++h) {
+            const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, off + 16 * h, 0, 0);
+            d.w[g][nb][4 * h + 0] = q.x;
+            d.w[g][nb][4 * h + 1] = q.y;
+            d.w[g][nb][4 * h + 2] = q.z;
+            d.w[g][nb][4 * h + 3] = q.w;
+          }
+        }
+        if (!a.zs_vec) {
+          d.z[g][nb] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(z_rsrc, zs_off[nb] + gg, 0, 0);
+          if constexpr (!DEBUGP)
+            d.s[g][nb] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(s_rsrc, (zs_off[nb] + gg) * 4u, 0, 0));
+        }
+      }
+    }
+    if (a.zs_vec) {
+      // the chunk's KCG zero points and scales of a column are contiguous:
+      // one or two vector loads per column instead of 2 * KCG scalar loads
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint32_t zo = zs_off[nb] + (uint32_t)(ch * KCG);
+        load_zero_run<KCG, NB>(z_rsrc, zo, d.z, nb);
+        if constexpr (!DEBUGP) load_scale_run<KCG, NB>(s_rsrc, zo * 4u, d.s, nb);
+      }
+    }
+  };
+
+  float acc[MB][NB][4];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[mb][nb][r] = 0.f;
+
+  // ---- one chunk of K ------------------------------------------------------
+  auto compute = [&](int ch, const int8_t* xb, const WChunk& wc) {
+#pragma unroll
+    for (int g = 0; g < KCG; ++g) {
+      const int gg = ch * KCG + g;
+      if (gg < a.G) {
+        i32x4 bfr[NB][S];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const ZeroFold zf = make_zero_fold(wc.z[g][nb]);
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            const uint32_t d0 = wc.w[g][nb][2 * s];
+            const uint32_t d1 = wc.w[g][nb][2 * s + 1];
+            bfr[nb][s].x = (int)fold_even(d0, zf);
+            bfr[nb][s].y = (int)fold_odd(d0, zf);
+            bfr[nb][s].z = (int)fold_even(d1, zf);
+            bfr[nb][s].w = (int)fold_odd(d1, zf);
+          }
+        }
+        // one 16-row block at a time: its int32 partials are folded into the
+        // fp32 accumulator right after its MFMAs, so only NB partials are live
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          i32x4 part[NB];
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            const i32x4 av = *reinterpret_cast<const i32x4*>(
+                xb + (mb * 16 + jl) * PITCH + g * GS + kb * (GS / 4) + 16 * s);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+              const i32x4 cin = (s == 0) ? i32x4{0, 0, 0, 0} : part[nb];
+              part[nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bfr[nb][s], cin, 0, 0, 0);
+            }
+          }
+          if constexpr (DEBUGP) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+              const int col = c.col0 + nb * 16 + jl;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int dst = s_dst[mb * 16 + kb * 4 + r];
+                if (dst >= 0 && col < a.N) a.dbg[((int64_t)dst * a.N + col) * a.G + gg] = part[nb][r];
+              }
+            }
+          } else {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                acc[mb][nb][r] = __builtin_fmaf((float)part[nb][r], wc.s[g][nb], acc[mb][nb][r]);
+          }
+        }
+      }
+    }
+  };
+
+  // ---- main loop: two chunks per iteration, ping-pong weight registers ----
+  WChunk wA, wB;
+  load_x(0);
+  load_w(0, wA);
+  for (int ch = 0; ch < c.nchunks; ch += 2) {
+    store_x(0);
+    __syncthreads();
+    if (ch + 1 < c.nchunks) {
+      load_x(ch + 1);
+      load_w(ch + 1, wB);
+    }
+    compute(ch, s_x, wA);
+    if (ch + 1 >= c.nchunks) break;
+    store_x(1);
+    __syncthreads();
+    if (ch + 2 < c.nchunks) {
+      load_x(ch + 2);
+      load_w(ch + 2, wA);
+    }
+    compute(ch + 1, s_x + BUF, wB);
+  }
+
+  if constexpr (!DEBUGP) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int col = c.col0 + nb * 16 + jl;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = mb * 16 + kb * 4 + r;
+          const int dst = s_dst[row];
+          if (dst >= 0 && col < a.N) {
+            float v = acc[mb][nb][r] * s_xs[row];
+            if constexpr (ROUTED) v = v * s_tw[row];
+            a.out[(int64_t)dst * a.ldo + col] = bf16_rne_bits(__float_as_uint(v));
+          }
+        }
+      }
+  }
+}
+
+template <int BM, int WN, int NW, int GS, int KCG, bool ROUTED, bool DEBUGP, int WAVES_PER_EU>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU)))
+void w4a8_gemm_kernel(const GemmArgs a) {
+  constexpr int BN = NW * WN;
+  constexpr int PITCH = KCG * GS + 16;
   static_assert(BM % 16 == 0 && WN % 16 == 0 && GS % 64 == 0, "tile shape");
 
-  __shared__ __attribute__((aligned(16))) int8_t s_x[2][BM * PITCH];
+  __shared__ __attribute__((aligned(16))) int8_t s_x[2 * BM * PITCH];
   __shared__ int s_src[BM];
   __shared__ int s_dst[BM];
   __shared__ float s_xs[BM];
   __shared__ float s_tw[BM];
+  __shared__ int s_rows;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int jl = lane & 15;   // row (A) / column (B) within a 16-block
-  const int kb = lane >> 4;   // K slot group of the MFMA operands
 
   // ---- tile decode -------------------------------------------------------
   const int L = blockIdx.x;
@@ -82,6 +372,8 @@ __global__ __launch_bounds__(NW * 64) void w4a8_gemm_kernel(const GemmArgs a) {
   }
   if (e < 0) return;
 
+  if (tid == 0) s_rows = 0;
+  __syncthreads();
   if (tid < BM) {
     int src = -1, dst = -1;
     float xsv = 0.f, twv = 1.f;
@@ -104,193 +396,23 @@ __global__ __launch_bounds__(NW * 64) void w4a8_gemm_kernel(const GemmArgs a) {
     s_dst[tid] = dst;
     s_xs[tid] = xsv;
     s_tw[tid] = twv;
+    if (dst >= 0) atomicMax(&s_rows, tid + 1);
   }
   __syncthreads();
+  const int rows = __builtin_amdgcn_readfirstlane(s_rows);
 
-  const int nchunks = (a.G + KCG - 1) / KCG;
-  const int col0 = nt * BN + wave * WN;
-  const int64_t khalf = a.K / 2;
-
-  // ---- activation chunk: global -> registers -> (relabelled) LDS ---------
-  u32x4 xr[XU];
-  auto load_x = [&](int ch) {
-#pragma unroll
-    for (int j = 0; j < XU; ++j) {
-      const int u = tid + j * NT;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (u < BM * UPR) {
-        const int row = u / UPR;
-        const int k = ch * KC + (u - row * UPR) * 16;
-        const int src = s_src[row];
-        if (src >= 0 && k < a.K) v = *reinterpret_cast<const u32x4*>(a.x + (int64_t)src * a.ldx + k);
-      }
-      xr[j] = v;
+  TileCtx c;
+  c.e = e;
+  c.col0 = nt * BN + wave * WN;
+  c.nchunks = (a.G + KCG - 1) / KCG;
+  // tiles whose valid rows fit in the top half run the half-height body
+  if constexpr (BM >= 64) {
+    if (rows <= BM / 2) {
+      gemm_body<BM / 2, BM, WN, NW, GS, KCG, ROUTED, DEBUGP>(a, c, s_x, s_src, s_dst, s_xs, s_tw);
+      return;
     }
-  };
-  auto store_x = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < XU; ++j) {
-      const int u = tid + j * NT;
-      if (u < BM * UPR) {
-        const int row = u / UPR;
-        const int c = u - row * UPR;
-        const u32x4 v = xr[j];
-        u32x4 p;
-        p.x = even_bytes(v.x, v.y);
-        p.y = odd_bytes(v.x, v.y);
-        p.z = even_bytes(v.z, v.w);
-        p.w = odd_bytes(v.z, v.w);
-        *reinterpret_cast<u32x4*>(&s_x[buf][row * PITCH + c * 16]) = p;
-      }
-    }
-  };
-
-  // ---- weights, zero points and scales of one chunk ----------------------
-  uint32_t wc[KCG][NB][WD], wn[KCG][NB][WD];
-  int zc[KCG][NB], zn[KCG][NB];
-  float sc[KCG][NB], sn[KCG][NB];
-  auto load_w = [&](int ch, uint32_t (&wd)[KCG][NB][WD], int (&zd)[KCG][NB], float (&sd)[KCG][NB]) {
-#pragma unroll
-    for (int g = 0; g < KCG; ++g) {
-      const int gg = ch * KCG + g;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int col = col0 + nb * 16 + jl;
-        const bool ok = gg < a.G && col < a.N;
-        const int64_t rowc = (int64_t)e * a.N + col;
-        if (ok) {
-          const uint8_t* p = a.w + rowc * khalf + (int64_t)gg * (GS / 2) + kb * (GS / 8);
-          if constexpr (S == 1) {
-            const u32x2 q = *reinterpret_cast<const u32x2*>(p);
-            wd[g][nb][0] = q.x;
-            wd[g][nb][1] = q.y;
-          } else {
-#pragma unroll
-            for (int h = 0; h < S / 2; ++h) {
-              const u32x4 q = *reinterpret_cast<const u32x4*>(p + 16 * h);
-              wd[g][nb][4 * h + 0] = q.x;
-              wd[g][nb][4 * h + 1] = q.y;
-              wd[g][nb][4 * h + 2] = q.z;
-              wd[g][nb][4 * h + 3] = q.w;
-            }
-          }
-          zd[g][nb] = a.wz[rowc * a.G + gg];
-          if constexpr (!DEBUGP) sd[g][nb] = a.ws[rowc * a.G + gg];
-        } else {
-#pragma unroll
-          for (int d = 0; d < WD; ++d) wd[g][nb][d] = 0u;
-          zd[g][nb] = 0;
-          sd[g][nb] = 0.f;
-        }
-      }
-    }
-  };
-
-  float acc[MB][NB][4];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[mb][nb][r] = 0.f;
-
-  load_x(0);
-  load_w(0, wc, zc, sc);
-
-  for (int ch = 0; ch < nchunks; ++ch) {
-    const int buf = ch & 1;
-    store_x(buf);
-    __syncthreads();
-    if (ch + 1 < nchunks) {
-      load_x(ch + 1);
-      load_w(ch + 1, wn, zn, sn);
-    }
-    const int8_t* xb = s_x[buf];
-#pragma unroll
-    for (int g = 0; g < KCG; ++g) {
-      const int gg = ch * KCG + g;
-      if (gg < a.G) {
-        i32x4 bfr[NB][S];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const ZeroFold zf = make_zero_fold(zc[g][nb]);
-#pragma unroll
-          for (int s = 0; s < S; ++s) {
-            const uint32_t d0 = wc[g][nb][2 * s];
-            const uint32_t d1 = wc[g][nb][2 * s + 1];
-            bfr[nb][s].x = (int)fold_even(d0, zf);
-            bfr[nb][s].y = (int)fold_odd(d0, zf);
-            bfr[nb][s].z = (int)fold_even(d1, zf);
-            bfr[nb][s].w = (int)fold_odd(d1, zf);
-          }
-        }
-        i32x4 part[MB][NB];
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb) {
-            const i32x4 av = *reinterpret_cast<const i32x4*>(
-                xb + (mb * 16 + jl) * PITCH + g * GS + kb * (GS / 4) + 16 * s);
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-              const i32x4 cin = (s == 0) ? i32x4{0, 0, 0, 0} : part[mb][nb];
-              part[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bfr[nb][s], cin, 0, 0, 0);
-            }
-          }
-        }
-        if constexpr (DEBUGP) {
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-              const int col = col0 + nb * 16 + jl;
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                const int dst = s_dst[mb * 16 + kb * 4 + r];
-                if (dst >= 0 && col < a.N)
-                  a.dbg[((int64_t)dst * a.N + col) * a.G + gg] = part[mb][nb][r];
-              }
-            }
-        } else {
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                acc[mb][nb][r] = __builtin_fmaf((float)part[mb][nb][r], sc[g][nb], acc[mb][nb][r]);
-        }
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < KCG; ++g)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-        for (int d = 0; d < WD; ++d) wc[g][nb][d] = wn[g][nb][d];
-        zc[g][nb] = zn[g][nb];
-        sc[g][nb] = sn[g][nb];
-      }
   }
-
-  if constexpr (!DEBUGP) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int col = col0 + nb * 16 + jl;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = mb * 16 + kb * 4 + r;
-          const int dst = s_dst[row];
-          if (dst >= 0 && col < a.N) {
-            float v = acc[mb][nb][r] * s_xs[row];
-            if constexpr (ROUTED) v = v * s_tw[row];
-            a.out[(int64_t)dst * a.ldo + col] = bf16_rne_bits(__float_as_uint(v));
-          }
-        }
-      }
-  }
+  gemm_body<BM, BM, WN, NW, GS, KCG, ROUTED, DEBUGP>(a, c, s_x, s_src, s_dst, s_xs, s_tw);
 }
 
 // ---------------------------------------------------------------------------
@@ -304,24 +426,28 @@ static void set_grid(GemmArgs& a, int max_blocks, int BN, int R) {
   a.per_xcd = (a.total_tiles + 7) / 8;
 }
 
-template <int BM, int WN, int NW, int GS, int KCG, bool ROUTED, bool DEBUGP>
+template <int BM, int WN, int NW, int GS, int KCG, bool ROUTED, bool DEBUGP, int WPE>
 static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   set_grid(a, max_blocks, NW * WN, R);
+  // a column's KCG zero points / scales of one chunk can be read as one
+  // aligned run when G is a multiple of KCG and both tensors are 16-byte aligned
+  a.zs_vec = (a.G % KCG == 0) && (reinterpret_cast<uintptr_t>(a.wz) % 16 == 0) &&
+             (reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
   if (a.total_tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, ROUTED, DEBUGP>), dim3(8 * a.per_xcd),
+  hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, ROUTED, DEBUGP, WPE>), dim3(8 * a.per_xcd),
                      dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
 
 template <int GS, bool ROUTED>
 static hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, hipStream_t s) {
-  // K-chunk sizes keep KCG * GS at 512 activation bytes per row for small
-  // row blocks and 256 for large ones.
+  // K-chunks: 1 KB of activations per row for small row blocks (deep weight
+  // prefetch for the HBM-bound regime), 256 bytes for large ones.
   switch (c.BM) {
-    case 16: return launch_one<16, 16, 4, GS, 512 / GS, ROUTED, false>(a, max_blocks, c.R, s);
-    case 32: return launch_one<32, 16, 4, GS, 512 / GS, ROUTED, false>(a, max_blocks, c.R, s);
-    case 64: return launch_one<64, 32, 4, GS, 256 / GS, ROUTED, false>(a, max_blocks, c.R, s);
-    case 128: return launch_one<128, 32, 4, GS, 256 / GS, ROUTED, false>(a, max_blocks, c.R, s);
+    case 16: return launch_one<16, 16, 4, GS, 1024 / GS, ROUTED, false, 1>(a, max_blocks, c.R, s);
+    case 32: return launch_one<32, 16, 4, GS, 512 / GS, ROUTED, false, 1>(a, max_blocks, c.R, s);
+    case 64: return launch_one<64, 32, 4, GS, 256 / GS, ROUTED, false, 2>(a, max_blocks, c.R, s);
+    case 128: return launch_one<128, 32, 4, GS, 256 / GS, ROUTED, false, 2>(a, max_blocks, c.R, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -338,9 +464,9 @@ hipError_t launch_grouped_gemm(GemmArgs a, const TileConfig& cfg, int group_size
 }
 
 hipError_t launch_debug_partials(GemmArgs a, int group_size, int max_blocks, hipStream_t s) {
-  if (group_size == 128) return launch_one<16, 16, 4, 128, 4, false, true>(a, max_blocks, 1, s);
-  if (group_size == 64) return launch_one<16, 16, 4, 64, 8, false, true>(a, max_blocks, 1, s);
-  if (group_size == 256) return launch_one<16, 16, 4, 256, 2, false, true>(a, max_blocks, 1, s);
+  if (group_size == 128) return launch_one<16, 16, 4, 128, 4, false, true, 1>(a, max_blocks, 1, s);
+  if (group_size == 64) return launch_one<16, 16, 4, 64, 8, false, true, 1>(a, max_blocks, 1, s);
+  if (group_size == 256) return launch_one<16, 16, 4, 256, 2, false, true, 1>(a, max_blocks, 1, s);
   return hipErrorInvalidValue;
 }
 
@@ -360,7 +486,7 @@ TileConfig select_tiles(int rows, int touched_experts, int N, int K, int group_s
   TileConfig c;
   c.NW = 4;
   if (per_expert <= 16) {
-    c.BM = 16; c.WN = 16; c.KCG = 512 / group_size; c.R = 1;
+    c.BM = 16; c.WN = 16; c.KCG = 1024 / group_size; c.R = 1;
   } else if (per_expert <= 32) {
     c.BM = 32; c.WN = 16; c.KCG = 512 / group_size; c.R = 1;
   } else if (per_expert <= 64) {

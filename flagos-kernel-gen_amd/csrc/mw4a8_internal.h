@@ -11,6 +11,7 @@ namespace mw4a8 {
 struct GemmArgs {
   const int8_t* x;        // [rows, K] int8, row stride ldx bytes
   int64_t ldx;
+  uint32_t x_bytes;       // rows * ldx (< 2^31)
   const float* xs;        // per-row activation scale
   const uint8_t* w;       // [E, N, K/2] packed int4
   const float* ws;        // [E, N, G] group scales
@@ -33,6 +34,7 @@ struct GemmArgs {
   int64_t ldo;
   int32_t* dbg;               // debug partials [rows, N, G] (debug kernels only)
   int N, K, G;
+  int zs_vec;                 // zero points/scales of a K-chunk load as one run (see zs_runs_ok)
   // launch geometry (see grid_for)
   int n_tiles, R, total_tiles, per_xcd;
 };

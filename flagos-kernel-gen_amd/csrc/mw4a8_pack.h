@@ -33,15 +33,26 @@
 
 namespace mw4a8 {
 
-// Bytes 0,2 of d0 and 0,2 of d1 -> one word (the even positions of an 8-byte run).
-MW4A8_HD uint32_t even_bytes(uint32_t d0, uint32_t d1) {
-  return (d0 & 0xffu) | ((d0 >> 8) & 0xff00u) | ((d1 & 0xffu) << 16) | ((d1 << 8) & 0xff000000u);
+// v_perm_b32: byte i of the result is byte sel[i] (0..7) of the 8-byte value
+// {hi, lo} (lo = bytes 0..3, hi = bytes 4..7). On the host this is a plain
+// emulation of the same selector semantics, so the CPU self-test checks the
+// selector constants the GPU uses.
+MW4A8_HD uint32_t byte_perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_perm(hi, lo, sel);
+#else
+  const uint64_t v = ((uint64_t)hi << 32) | lo;
+  uint32_t r = 0;
+  for (int i = 0; i < 4; ++i) r |= (uint32_t)((v >> (8 * ((sel >> (8 * i)) & 7))) & 0xffu) << (8 * i);
+  return r;
+#endif
 }
 
+// Bytes 0,2 of d0 and 0,2 of d1 -> one word (the even positions of an 8-byte run).
+MW4A8_HD uint32_t even_bytes(uint32_t d0, uint32_t d1) { return byte_perm(d1, d0, 0x06040200u); }
+
 // Bytes 1,3 of d0 and 1,3 of d1 -> one word (the odd positions of an 8-byte run).
-MW4A8_HD uint32_t odd_bytes(uint32_t d0, uint32_t d1) {
-  return ((d0 >> 8) & 0xffu) | ((d0 >> 16) & 0xff00u) | ((d1 << 8) & 0xff0000u) | (d1 & 0xff000000u);
-}
+MW4A8_HD uint32_t odd_bytes(uint32_t d0, uint32_t d1) { return byte_perm(d1, d0, 0x07050301u); }
 
 // Per-(column, group) constants of the zero-point fold.
 struct ZeroFold {
