@@ -106,24 +106,36 @@ __device__ __forceinline__ void load_scale_run(__amdgpu_buffer_rsrc_t r, uint32_
 struct TileCtx {
   int e;          // expert
   int col0;       // first column of this wave
+  int tile_col0;  // first column of the workgroup's tile
   int nchunks;    // K-chunks
+  int rows;       // rows of the tile holding data (the rest is padding)
 };
 
 // Main K loop and epilogue for the first BMX rows of a tile (BMX <= BM).
-template <int BMX, int BM, int WN, int NW, int GS, int KCG, bool ROUTED, bool DEBUGP>
-__device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, int8_t* s_x, const int* s_src,
-                                          const int* s_dst, const float* s_xs, const float* s_tw) {
+//
+// RD: weight-register ring depth. The weights (and, unless ZS_LDS, the zero
+//     points and scales) of chunk c + RD - 1 are requested while chunk c is
+//     computed.
+// ZSG: when positive, the tile's whole [BN x G] zero-point and scale block
+//     (G <= ZSG) is copied into LDS once -- it is contiguous in memory -- so
+//     the K loop issues no loads for them. When zero they travel with the
+//     weights, one vector run per column and chunk when aligned.
+template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, bool ROUTED, bool DEBUGP>
+__device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, int8_t* s_x, float* s_scale,
+                                          int8_t* s_zero, const int* s_src, const int* s_dst, const float* s_xs,
+                                          const float* s_tw) {
   constexpr int NT = NW * 64;
   constexpr int MB = BMX / 16;        // 16-row blocks computed
   constexpr int NB = WN / 16;         // 16-column blocks per wave
+  constexpr int BN = NW * WN;
   constexpr int S = GS / 64;          // MFMA K-steps per group
   constexpr int WD = 2 * S;           // packed dwords per lane per (group, column block)
   constexpr int KC = KCG * GS;        // activation bytes per row per chunk
   constexpr int PITCH = KC + 16;      // LDS row pitch in bytes
   constexpr int BUF = BM * PITCH;     // bytes per LDS buffer
   constexpr int UPR = KC / 16;        // 16-byte units per row and chunk
-  constexpr int XU = (BMX * UPR) / NT;
-  static_assert((BMX * UPR) % NT == 0, "activation chunk must split evenly over the workgroup");
+  constexpr int XU = (BMX * UPR + NT - 1) / NT;
+  constexpr bool ZS_LDS = ZSG > 0;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -149,35 +161,68 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     w_off[nb] = ok ? (uint32_t)col * khalf + (uint32_t)(kb * (GS / 8)) : kOOB;
     zs_off[nb] = ok ? (uint32_t)(col * a.G) : kOOB;
   }
+  // only rows that hold data are staged; padding rows stay whatever LDS holds
+  // and their results are never stored
+  const int xunits = min(c.rows, BMX) * UPR;
   uint32_t x_off[XU];
 #pragma unroll
   for (int j = 0; j < XU; ++j) {
     const int u = tid + j * NT;
-    const int row = u / UPR;
+    const int row = min(u / UPR, BMX - 1);
     const int src = s_src[row];
-    x_off[j] = src >= 0 ? (uint32_t)(src * a.ldx) + (uint32_t)((u - row * UPR) * 16) : kOOB;
+    x_off[j] = src >= 0 ? (uint32_t)(src * a.ldx) + (uint32_t)((u - (u / UPR) * UPR) * 16) : kOOB;
   }
+
+  // ---- the tile's zero points and scales -> registers (ZS_LDS) -------------
+  // [BN columns x G] of each, contiguous from column tile_col0; the
+  // descriptors return zero past column N. All loads are issued before any
+  // LDS write so their latencies overlap (and overlap the pipeline prologue).
+  constexpr int SU = ZS_LDS ? (BN * ZSG / 4 + NT - 1) / NT : 1;    // scale units per thread
+  constexpr int ZU = ZS_LDS ? (BN * ZSG / 16 + NT - 1) / NT : 1;   // zero-point units per thread
+  const int s_units = BN * a.G / 4;
+  const int z_units = BN * a.G / 16;
+  u32x4 sq[SU], zq[ZU];
+  if constexpr (ZS_LDS) {
+    const uint32_t zbase = (uint32_t)(c.tile_col0 * a.G);
+#pragma unroll
+    for (int j = 0; j < SU; ++j) {
+      const int u = tid + j * NT;
+      if (!DEBUGP && u < s_units) sq[j] = __builtin_amdgcn_raw_buffer_load_b128(s_rsrc, zbase * 4u + u * 16u, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < ZU; ++j) {
+      const int u = tid + j * NT;
+      if (u < z_units) zq[j] = __builtin_amdgcn_raw_buffer_load_b128(z_rsrc, zbase + u * 16u, 0, 0);
+    }
+  }
+  // LDS index of this lane's columns in the zero/scale block
+  int zs_lds[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) zs_lds[nb] = (c.col0 - c.tile_col0 + nb * 16 + jl) * a.G;
 
   // ---- chunk loaders -----------------------------------------------------
   u32x4 xr[XU];
   auto load_x = [&](int ch) {
 #pragma unroll
     for (int j = 0; j < XU; ++j)
-      xr[j] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, x_off[j] + (uint32_t)(ch * KC), 0, 0);
+      if (tid + j * NT < xunits)
+        xr[j] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, x_off[j] + (uint32_t)(ch * KC), 0, 0);
   };
   auto store_x = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < XU; ++j) {
       const int u = tid + j * NT;
-      const int row = u / UPR;
-      const int cu = u - row * UPR;
-      const u32x4 v = xr[j];
-      u32x4 p;
-      p.x = even_bytes(v.x, v.y);
-      p.y = odd_bytes(v.x, v.y);
-      p.z = even_bytes(v.z, v.w);
-      p.w = odd_bytes(v.z, v.w);
-      *reinterpret_cast<u32x4*>(s_x + buf * BUF + row * PITCH + cu * 16) = p;
+      if (u < xunits) {
+        const int row = u / UPR;
+        const int cu = u - row * UPR;
+        const u32x4 v = xr[j];
+        u32x4 p;
+        p.x = even_bytes(v.x, v.y);
+        p.y = odd_bytes(v.x, v.y);
+        p.z = even_bytes(v.z, v.w);
+        p.w = odd_bytes(v.z, v.w);
+        *reinterpret_cast<u32x4*>(s_x + buf * BUF + row * PITCH + cu * 16) = p;
+      }
     }
   };
 
@@ -207,14 +252,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
             d.w[g][nb][4 * h + 3] = q.w;
           }
         }
-        if (!a.zs_vec) {
+        if (!ZS_LDS && !a.zs_vec) {
           d.z[g][nb] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(z_rsrc, zs_off[nb] + gg, 0, 0);
           if constexpr (!DEBUGP)
             d.s[g][nb] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(s_rsrc, (zs_off[nb] + gg) * 4u, 0, 0));
         }
       }
     }
-    if (a.zs_vec) {
+    if (!ZS_LDS && a.zs_vec) {
       // the chunk's KCG zero points and scales of a column are contiguous:
       // one or two vector loads per column instead of 2 * KCG scalar loads
 #pragma unroll
@@ -240,10 +285,22 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     for (int g = 0; g < KCG; ++g) {
       const int gg = ch * KCG + g;
       if (gg < a.G) {
+        int zv[NB];
+        float sv[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          if constexpr (ZS_LDS) {
+            zv[nb] = s_zero[zs_lds[nb] + gg];
+            sv[nb] = s_scale[zs_lds[nb] + gg];
+          } else {
+            zv[nb] = wc.z[g][nb];
+            sv[nb] = wc.s[g][nb];
+          }
+        }
         i32x4 bfr[NB][S];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-          const ZeroFold zf = make_zero_fold(wc.z[g][nb]);
+          const ZeroFold zf = make_zero_fold(zv[nb]);
 #pragma unroll
           for (int s = 0; s < S; ++s) {
             const uint32_t d0 = wc.w[g][nb][2 * s];
@@ -284,33 +341,44 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
             for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
               for (int r = 0; r < 4; ++r)
-                acc[mb][nb][r] = __builtin_fmaf((float)part[nb][r], wc.s[g][nb], acc[mb][nb][r]);
+                acc[mb][nb][r] = __builtin_fmaf((float)part[nb][r], sv[nb], acc[mb][nb][r]);
           }
         }
       }
     }
   };
 
-  // ---- main loop: two chunks per iteration, ping-pong weight registers ----
-  WChunk wA, wB;
+  // ---- main loop: chunk c uses ring slot c % RD ----------------------------
+  WChunk ring[RD];
   load_x(0);
-  load_w(0, wA);
-  for (int ch = 0; ch < c.nchunks; ch += 2) {
-    store_x(0);
-    __syncthreads();
-    if (ch + 1 < c.nchunks) {
-      load_x(ch + 1);
-      load_w(ch + 1, wB);
+#pragma unroll
+  for (int d = 0; d < RD - 1; ++d)
+    if (d < c.nchunks) load_w(d, ring[d]);
+  if constexpr (ZS_LDS) {
+    // visible to all waves after the first barrier of the loop
+#pragma unroll
+    for (int j = 0; j < SU; ++j) {
+      const int u = tid + j * NT;
+      if (!DEBUGP && u < s_units) *reinterpret_cast<u32x4*>(s_scale + 4 * u) = sq[j];
     }
-    compute(ch, s_x, wA);
-    if (ch + 1 >= c.nchunks) break;
-    store_x(1);
-    __syncthreads();
-    if (ch + 2 < c.nchunks) {
-      load_x(ch + 2);
-      load_w(ch + 2, wA);
+#pragma unroll
+    for (int j = 0; j < ZU; ++j) {
+      const int u = tid + j * NT;
+      if (u < z_units) *reinterpret_cast<u32x4*>(s_zero + 16 * u) = zq[j];
     }
-    compute(ch + 1, s_x + BUF, wB);
+  }
+  for (int ch = 0; ch < c.nchunks; ch += RD) {
+#pragma unroll
+    for (int d = 0; d < RD; ++d) {
+      const int cc = ch + d;
+      if (cc < c.nchunks) {
+        store_x(cc & 1);
+        __syncthreads();
+        if (cc + 1 < c.nchunks) load_x(cc + 1);
+        if (cc + RD - 1 < c.nchunks) load_w(cc + RD - 1, ring[(d + RD - 1) % RD]);
+        compute(cc, s_x + (cc & 1) * BUF, ring[d]);
+      }
+    }
   }
 
   if constexpr (!DEBUGP) {
@@ -333,14 +401,19 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   }
 }
 
-template <int BM, int WN, int NW, int GS, int KCG, bool ROUTED, bool DEBUGP, int WAVES_PER_EU>
+// ZSG > 0: zero points and scales come from an LDS copy of the tile's
+// block; the host launches this only when G <= ZSG (see zs_block_fits).
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, bool ROUTED, bool DEBUGP, int WAVES_PER_EU>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU)))
 void w4a8_gemm_kernel(const GemmArgs a) {
   constexpr int BN = NW * WN;
   constexpr int PITCH = KCG * GS + 16;
+  constexpr bool ZS_LDS = ZSG > 0;
   static_assert(BM % 16 == 0 && WN % 16 == 0 && GS % 64 == 0, "tile shape");
 
   __shared__ __attribute__((aligned(16))) int8_t s_x[2 * BM * PITCH];
+  __shared__ __attribute__((aligned(16))) float s_scale[ZS_LDS ? BN * ZSG : 4];
+  __shared__ __attribute__((aligned(16))) int8_t s_zero[ZS_LDS ? BN * ZSG : 16];
   __shared__ int s_src[BM];
   __shared__ int s_dst[BM];
   __shared__ float s_xs[BM];
@@ -403,16 +476,19 @@ void w4a8_gemm_kernel(const GemmArgs a) {
 
   TileCtx c;
   c.e = e;
+  c.tile_col0 = nt * BN;
   c.col0 = nt * BN + wave * WN;
   c.nchunks = (a.G + KCG - 1) / KCG;
+  c.rows = rows;
   // tiles whose valid rows fit in the top half run the half-height body
   if constexpr (BM >= 64) {
     if (rows <= BM / 2) {
-      gemm_body<BM / 2, BM, WN, NW, GS, KCG, ROUTED, DEBUGP>(a, c, s_x, s_src, s_dst, s_xs, s_tw);
+      gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP>(a, c, s_x, s_scale, s_zero, s_src, s_dst,
+                                                                     s_xs, s_tw);
       return;
     }
   }
-  gemm_body<BM, BM, WN, NW, GS, KCG, ROUTED, DEBUGP>(a, c, s_x, s_src, s_dst, s_xs, s_tw);
+  gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP>(a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs, s_tw);
 }
 
 // ---------------------------------------------------------------------------
@@ -426,7 +502,14 @@ static void set_grid(GemmArgs& a, int max_blocks, int BN, int R) {
   a.per_xcd = (a.total_tiles + 7) / 8;
 }
 
-template <int BM, int WN, int NW, int GS, int KCG, bool ROUTED, bool DEBUGP, int WPE>
+// The tile's [BN x G] zero-point/scale block can be copied to an LDS array of
+// BN * ZSG entries in whole 16-byte units from 16-byte-aligned addresses.
+static bool zs_block_fits(const GemmArgs& a, int BN, int ZSG) {
+  return ZSG > 0 && a.G <= ZSG && (BN * a.G) % 16 == 0 && (a.N * a.G) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(a.wz) % 16 == 0 && (a.ws == nullptr || reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
+}
+
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, bool ROUTED, bool DEBUGP, int WPE>
 static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   set_grid(a, max_blocks, NW * WN, R);
   // a column's KCG zero points / scales of one chunk can be read as one
@@ -434,20 +517,30 @@ static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   a.zs_vec = (a.G % KCG == 0) && (reinterpret_cast<uintptr_t>(a.wz) % 16 == 0) &&
              (reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
   if (a.total_tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, ROUTED, DEBUGP, WPE>), dim3(8 * a.per_xcd),
+  hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP, WPE>), dim3(8 * a.per_xcd),
                      dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
 
 template <int GS, bool ROUTED>
 static hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, hipStream_t s) {
-  // K-chunks: 1 KB of activations per row for small row blocks (deep weight
-  // prefetch for the HBM-bound regime), 256 bytes for large ones.
+  constexpr int K512 = 512 / GS > 0 ? 512 / GS : 1;     // groups per 512 bytes of K
+  constexpr int K1024 = 1024 / GS > 0 ? 1024 / GS : 1;
+  constexpr int K256 = 256 / GS > 0 ? 256 / GS : 1;
   switch (c.BM) {
-    case 16: return launch_one<16, 16, 4, GS, 1024 / GS, ROUTED, false, 1>(a, max_blocks, c.R, s);
-    case 32: return launch_one<32, 16, 4, GS, 512 / GS, ROUTED, false, 1>(a, max_blocks, c.R, s);
-    case 64: return launch_one<64, 32, 4, GS, 256 / GS, ROUTED, false, 2>(a, max_blocks, c.R, s);
-    case 128: return launch_one<128, 32, 4, GS, 256 / GS, ROUTED, false, 2>(a, max_blocks, c.R, s);
+    case 16:
+      if (zs_block_fits(a, 64, 64)) {
+        // few tiles (decode of a handful of tokens): deeper chunks per wave
+        if ((int64_t)max_blocks * ((a.N + 63) / 64) < 1024)
+          return launch_one<16, 16, 4, GS, K1024, 2, 64, ROUTED, false, 1>(a, max_blocks, c.R, s);
+        return launch_one<16, 16, 4, GS, K512, 2, 64, ROUTED, false, 1>(a, max_blocks, c.R, s);
+      }
+      return launch_one<16, 16, 4, GS, K1024, 2, 0, ROUTED, false, 1>(a, max_blocks, c.R, s);
+    case 32:
+      if (zs_block_fits(a, 64, 64)) return launch_one<32, 16, 4, GS, K512, 2, 64, ROUTED, false, 1>(a, max_blocks, c.R, s);
+      return launch_one<32, 16, 4, GS, K512, 2, 0, ROUTED, false, 1>(a, max_blocks, c.R, s);
+    case 64: return launch_one<64, 32, 4, GS, K256, 2, 0, ROUTED, false, 2>(a, max_blocks, c.R, s);
+    case 128: return launch_one<128, 32, 4, GS, K256, 2, 0, ROUTED, false, 2>(a, max_blocks, c.R, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -464,9 +557,9 @@ hipError_t launch_grouped_gemm(GemmArgs a, const TileConfig& cfg, int group_size
 }
 
 hipError_t launch_debug_partials(GemmArgs a, int group_size, int max_blocks, hipStream_t s) {
-  if (group_size == 128) return launch_one<16, 16, 4, 128, 4, false, true, 1>(a, max_blocks, 1, s);
-  if (group_size == 64) return launch_one<16, 16, 4, 64, 8, false, true, 1>(a, max_blocks, 1, s);
-  if (group_size == 256) return launch_one<16, 16, 4, 256, 2, false, true, 1>(a, max_blocks, 1, s);
+  if (group_size == 128) return launch_one<16, 16, 4, 128, 4, 2, 0, false, true, 1>(a, max_blocks, 1, s);
+  if (group_size == 64) return launch_one<16, 16, 4, 64, 8, 2, 0, false, true, 1>(a, max_blocks, 1, s);
+  if (group_size == 256) return launch_one<16, 16, 4, 256, 2, 2, 0, false, true, 1>(a, max_blocks, 1, s);
   return hipErrorInvalidValue;
 }
 

@@ -34,7 +34,7 @@ struct GemmArgs {
   int64_t ldo;
   int32_t* dbg;               // debug partials [rows, N, G] (debug kernels only)
   int N, K, G;
-  int zs_vec;                 // zero points/scales of a K-chunk load as one run (see zs_runs_ok)
+  int zs_vec;                 // zero points/scales of a K-chunk load as one vector run per column
   // launch geometry (see grid_for)
   int n_tiles, R, total_tiles, per_xcd;
 };

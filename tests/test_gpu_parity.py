@@ -134,6 +134,34 @@ def test_grouped_edge_cases(pkg, dev):
     assert_close(out, ref, 512, "edge/strided x")
 
 
+@pytest.mark.parametrize("case", ["misaligned", "many_groups"])
+def test_grouped_scale_zero_fallback_paths(pkg, dev, case):
+    """Zero points/scales that cannot use the tile-block LDS copy (a group
+    count above its capacity, or tensors not 16-byte aligned) take the
+    per-chunk load path."""
+    wl = pkg.workloads
+    if case == "many_groups":
+        E, M, N, K, gs = 3, 40, 256, 9216, 128          # G = 72
+    else:
+        E, M, N, K, gs = 4, 48, 512, 1024, 128
+    x_q, x_scale, w_q4, w_scale, w_zero, offs = wl.make_grouped_inputs(E, M, N, K, gs, seed=81, zero="full")
+    ws_d, wz_d = w_scale.to(dev), w_zero.to(dev)
+    if case == "misaligned":
+        # same values, storage shifted off 16-byte alignment
+        ws_big = torch.empty(ws_d.numel() + 1, dtype=torch.float32, device=dev)
+        ws_big[1:] = ws_d.reshape(-1)
+        ws_d = ws_big[1:].view(ws_d.shape)
+        wz_big = torch.empty(wz_d.numel() + 3, dtype=torch.int8, device=dev)
+        wz_big[3:] = wz_d.reshape(-1)
+        wz_d = wz_big[3:].view(wz_d.shape)
+        assert ws_d.data_ptr() % 16 != 0 and wz_d.data_ptr() % 16 != 0
+    ref = task1_ref.w4a8_group_gemm_moe_ref(x_q, x_scale, w_q4, w_scale, w_zero, offs,
+                                            torch.zeros(M, N, dtype=torch.bfloat16), gs)
+    out = torch.zeros(M, N, dtype=torch.bfloat16, device=dev)
+    pkg.w4a8_group_gemm_moe(x_q.to(dev), x_scale.to(dev), w_q4.to(dev), ws_d, wz_d, offs.to(dev), out, gs)
+    assert_close(out, ref, N, case)
+
+
 @pytest.mark.parametrize("rows_per_expert", [8, 24, 60, 200])
 def test_grouped_every_block_size(pkg, dev, rows_per_expert):
     """Row counts that select each of the 16/32/64/128 row-block kernels."""
