@@ -27,9 +27,10 @@
 // register sets (the loop is unrolled by two chunks, so no copies), and LDS
 // is double-buffered, so one barrier per chunk suffices.
 //
-// Grid: a 1-D list of (row block, column tile) pairs, a multiple of 8 long.
-// Workgroup L runs on XCD L % 8, so tile t = (L % 8) * per_xcd + L / 8 gives
-// every XCD a contiguous run of the list. The list walks R row blocks
+// Grid: a 1-D list of (row block, column tile) pairs, sized on the host for
+// the worst-case number of row blocks. Workgroup L runs on XCD L % 8; with
+// per_xcd = ceil(actual tiles / 8), tile t = (L % 8) * per_xcd + L / 8 gives
+// every XCD an equal, contiguous run of the actual tiles. The list walks R row blocks
 // (usually of one expert) across all column tiles before moving on, so the
 // activation rows and the weight tile a row block pair shares stay in that
 // XCD's L2.
@@ -311,21 +312,17 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
             bfr[nb][s].w = (int)fold_odd(d1, zf);
           }
         }
-        // one 16-row block at a time: its int32 partials are folded into the
-        // fp32 accumulator right after its MFMAs, so only NB partials are live
+        // Software-pipelined over 16-row blocks: the A fragments of block
+        // mb+1 are read from LDS while block mb's MFMAs run, and block mb-1's
+        // int32 partials are folded into the fp32 accumulators after block
+        // mb's MFMAs are issued, so neither the LDS latency nor the MFMA
+        // result latency sits on the issue path.
+        const int8_t* xg = xb + jl * PITCH + g * GS + kb * (GS / 4);
+        auto read_a = [&](int mb, i32x4 (&av)[S]) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          i32x4 part[NB];
-#pragma unroll
-          for (int s = 0; s < S; ++s) {
-            const i32x4 av = *reinterpret_cast<const i32x4*>(
-                xb + (mb * 16 + jl) * PITCH + g * GS + kb * (GS / 4) + 16 * s);
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-              const i32x4 cin = (s == 0) ? i32x4{0, 0, 0, 0} : part[nb];
-              part[nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bfr[nb][s], cin, 0, 0, 0);
-            }
-          }
+          for (int s = 0; s < S; ++s) av[s] = *reinterpret_cast<const i32x4*>(xg + mb * 16 * PITCH + 16 * s);
+        };
+        auto fold = [&](int mb, const i32x4 (&part)[NB]) {
           if constexpr (DEBUGP) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
@@ -343,7 +340,23 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
               for (int r = 0; r < 4; ++r)
                 acc[mb][nb][r] = __builtin_fmaf((float)part[nb][r], sv[nb], acc[mb][nb][r]);
           }
+        };
+        i32x4 av[2][S];
+        i32x4 part[2][NB];
+        read_a(0, av[0]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          if (mb + 1 < MB) read_a(mb + 1, av[(mb + 1) & 1]);
+#pragma unroll
+          for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+              const i32x4 cin = (s == 0) ? i32x4{0, 0, 0, 0} : part[mb & 1][nb];
+              part[mb & 1][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mb & 1][s], bfr[nb][s], cin, 0, 0, 0);
+            }
+          if (mb > 0) fold(mb - 1, part[(mb - 1) & 1]);
         }
+        fold(MB - 1, part[(MB - 1) & 1]);
       }
     }
   };
@@ -424,23 +437,33 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   // ---- tile decode -------------------------------------------------------
-  const int L = blockIdx.x;
-  const int t = (L & 7) * a.per_xcd + (L >> 3);
-  if (t >= a.total_tiles) return;
+  // The grid covers the worst-case block count; the actual count is only
+  // known here. Spread the actual tiles evenly over the 8 XCDs (workgroup L
+  // runs on XCD L % 8), each XCD taking a contiguous run of the tile list.
+  int nblocks;
+  if constexpr (ROUTED) {
+    // blocks past sorted_len / BM would read past sorted_ids / expert_ids
+    nblocks = min(a.num_post_pad[0] / BM, a.sorted_len / BM);
+  } else {
+    nblocks = a.blk_count[0];
+  }
   const int span = a.n_tiles * a.R;
+  const int tiles = (nblocks + a.R - 1) / a.R * span;
+  const int per_xcd = (tiles + 7) >> 3;
+  const int L = blockIdx.x;
+  if ((L >> 3) >= per_xcd) return;
+  const int t = (L & 7) * per_xcd + (L >> 3);
+  if (t >= tiles) return;
   const int chunk_id = t / span;
   const int rem = t - chunk_id * span;
   const int nt = rem / a.R;
   const int b = chunk_id * a.R + (rem - nt * a.R);
+  if (b >= nblocks) return;
   int e;
   if constexpr (ROUTED) {
-    // (b + 1) * BM <= sorted_len also bounds expert_ids, whose length is
-    // ceil(sorted_len / BM)
-    if (b >= a.num_post_pad[0] / BM || (int64_t)(b + 1) * BM > a.sorted_len) return;
     e = a.expert_ids[b];
     if (e >= a.E) return;
   } else {
-    if (b >= a.blk_count[0]) return;
     e = a.blk_expert[b];
   }
   if (e < 0) return;
