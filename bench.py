@@ -215,6 +215,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--headline-only", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 1 GiB int32 read+write kernel (torch.neg) to calibrate "
+                         "rocprofv3 FETCH_SIZE/WRITE_SIZE against known bytes")
     ap.add_argument("--workload", default=None,
                     help="name:M to measure instead of the headline (profiling); implies --headline-only")
     args = ap.parse_args()
@@ -250,6 +253,14 @@ def main():
             log(json.dumps(points[-1]))
             del pt
             torch.cuda.empty_cache()
+
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     cpu = None
     if not args.no_cpu:
