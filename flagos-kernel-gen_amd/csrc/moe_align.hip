@@ -2,17 +2,19 @@
 //
 // moe_align_kernel: token-expert pairs -> expert-sorted, block-padded slots.
 //   One workgroup of 1024 threads (16 wave64s):
-//   1. LDS histogram of expert ids (ids outside [0, E) are not routed).
+//   1. Per-wave LDS histograms of expert ids (ids outside [0, E) are not
+//      routed).
 //   2. Workgroup scan of per-expert block counts and pair counts.
 //   3. Padding slots, expert_ids and the tails of both buffers are written
 //      directly from the scan (each expert owns at most BM-1 padding slots).
-//   4. Stable scatter in rounds of 1024 consecutive pairs. Inside a wave the
-//      lanes holding the same expert are found with one ballot per id bit;
-//      a lane's rank is the popcount of its peers below it. Wave counts go
-//      through LDS so later waves add the counts of earlier ones, and a
-//      running per-expert cursor carries counts across rounds. Slot order
-//      within an expert is therefore ascending pair index, independent of
-//      scheduling, which makes the output bit-exact with a stable sort.
+//   4. Stable scatter: wave w owns a contiguous range of pairs and its own
+//      per-expert cursors, which start at the expert's padded offset plus the
+//      counts of the waves before w. Inside a wave the lanes holding the same
+//      expert are found with one ballot per id bit; a lane's rank is the
+//      popcount of its peers below it. Slot order within an expert is
+//      therefore ascending pair index, independent of scheduling, which makes
+//      the output bit-exact with a stable sort. No workgroup barrier is
+//      needed after the scan.
 //
 // csr_block_table_kernel: CSR expert_offsets (reference layout,
 //   docs/Task1.md:87-92) -> list of (expert, first row, end row) blocks of
@@ -24,6 +26,7 @@ namespace mw4a8 {
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / 64;
 constexpr int kAlignMaxE = 1024;
+constexpr int kAlignCachedPairs = 32768;   // ids kept in LDS (16 bits each) up to this many pairs
 
 // Exclusive scan of one int per thread across a 1024-thread workgroup.
 // `wave_sums` must hold kAlignWaves ints. Returns the exclusive prefix and
@@ -60,59 +63,89 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
     int32_t* __restrict__ sorted_ids, int sorted_len,
     int32_t* __restrict__ expert_ids, int blocks_len,
     int32_t* __restrict__ num_post_pad, int32_t* __restrict__ expert_offsets) {
-  __shared__ int s_cnt[kAlignMaxE];
-  __shared__ int s_cur[kAlignMaxE];
-  __shared__ int s_boff[kAlignMaxE + 1];
-  __shared__ uint8_t s_wcnt[kAlignWaves][kAlignMaxE];
+  // per-wave expert counts; after the scan, each wave's next free slot per expert
+  __shared__ int s_wcnt[kAlignWaves][kAlignMaxE];
   __shared__ int s_wave[kAlignWaves];
+  // the pairs' expert ids, read once from HBM (0xffff = not routed)
+  __shared__ uint16_t s_ids[kAlignCachedPairs];
+  const bool cached = P <= kAlignCachedPairs;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
-  for (int e = tid; e < E; e += kAlignThreads) { s_cnt[e] = 0; s_cur[e] = 0; }
-  for (int i = tid; i < kAlignWaves * kAlignMaxE / 4; i += kAlignThreads)
-    reinterpret_cast<int*>(&s_wcnt[0][0])[i] = 0;
+  for (int i = tid; i < kAlignWaves * kAlignMaxE; i += kAlignThreads) (&s_wcnt[0][0])[i] = 0;
   __syncthreads();
 
-  // 1. histogram
-  for (int i = tid; i < P; i += kAlignThreads) {
-    const int e = topk_ids[i];
-    if ((unsigned)e < (unsigned)E) atomicAdd(&s_cnt[e], 1);
+  // wave w owns the contiguous pair range [p0, p1)
+  const int seg = (P + kAlignWaves - 1) / kAlignWaves;
+  const int p0 = min(P, wave * seg);
+  const int p1 = min(P, p0 + seg);
+
+  // 1. per-wave histograms (ids outside [0, E) are not routed)
+  // eight independent loads in flight per lane before any of them is used
+  constexpr int kBatch = 8;
+  for (int i0 = p0 + lane; i0 < p1; i0 += 64 * kBatch) {
+    int ev[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int i = i0 + 64 * j;
+      ev[j] = i < p1 ? topk_ids[i] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int i = i0 + 64 * j;
+      const bool ok = (unsigned)ev[j] < (unsigned)E;
+      if (cached && i < p1) s_ids[i] = ok ? (uint16_t)ev[j] : (uint16_t)0xffff;
+      if (ok) atomicAdd(&s_wcnt[wave][ev[j]], 1);
+    }
   }
   __syncthreads();
 
-  // 2. scans (E <= 1024: one expert per thread)
-  const int my_cnt = tid < E ? s_cnt[tid] : 0;
+  // 2. per-expert totals, block and pair offsets (E <= 1024: one expert per
+  //    thread), then each wave's first slot for the expert: the expert's
+  //    padded start plus the counts of the waves before it
+  int my_cnt = 0;
+  if (tid < E) {
+#pragma unroll
+    for (int w = 0; w < kAlignWaves; ++w) my_cnt += s_wcnt[w][tid];
+  }
   const int my_blk = (my_cnt + BM - 1) / BM;
   int tot_blk, tot_cnt;
   const int blk_ex = block_exclusive_scan(my_blk, s_wave, &tot_blk);
   const int cnt_ex = block_exclusive_scan(my_cnt, s_wave, &tot_cnt);
   if (tid < E) {
-    s_boff[tid] = blk_ex;
+    int run = blk_ex * BM;
+#pragma unroll
+    for (int w = 0; w < kAlignWaves; ++w) {
+      const int c = s_wcnt[w][tid];
+      s_wcnt[w][tid] = run;
+      run += c;
+    }
     if (expert_offsets) expert_offsets[tid] = cnt_ex;
+    const int first = blk_ex * BM;
+    for (int sl = first + my_cnt; sl < first + my_blk * BM; ++sl) sorted_ids[sl] = P;
+    for (int bb = blk_ex; bb < blk_ex + my_blk; ++bb) expert_ids[bb] = tid;
   }
   if (tid == 0) {
-    s_boff[E] = tot_blk;
     if (expert_offsets) expert_offsets[E] = tot_cnt;
     num_post_pad[0] = tot_blk * BM;
   }
+  for (int sl = tot_blk * BM + tid; sl < sorted_len; sl += kAlignThreads) sorted_ids[sl] = P;
+  for (int bb = tot_blk + tid; bb < blocks_len; bb += kAlignThreads) expert_ids[bb] = -1;
   __syncthreads();
 
-  // 3. padding slots, block owners, buffer tails
-  if (tid < E) {
-    const int first = blk_ex * BM;
-    for (int s = first + my_cnt; s < first + my_blk * BM; ++s) sorted_ids[s] = P;
-    for (int b = blk_ex; b < blk_ex + my_blk; ++b) expert_ids[b] = tid;
-  }
-  for (int s = tot_blk * BM + tid; s < sorted_len; s += kAlignThreads) sorted_ids[s] = P;
-  for (int b = tot_blk + tid; b < blocks_len; b += kAlignThreads) expert_ids[b] = -1;
-
-  // 4. stable scatter
+  // 3. stable scatter, each wave on its own range and its own cursors (no
+  //    workgroup barriers): the lanes holding the same expert are found with
+  //    one ballot per id bit; a lane's slot is the wave's cursor plus the
+  //    number of such lanes below it, and the lowest of them advances the
+  //    cursor. The read of the cursor by every lane precedes the leader's
+  //    write in the wave's LDS instruction order.
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int base = 0; base < P; base += kAlignThreads) {
-    const int i = base + tid;
-    const int e = i < P ? topk_ids[i] : -1;
+  for (int base = p0; base < p1; base += 64) {
+    const int i = base + lane;
+    int e = -1;
+    if (i < p1) e = cached ? (s_ids[i] == 0xffff ? -1 : (int)s_ids[i]) : topk_ids[i];
     const bool valid = (unsigned)e < (unsigned)E;
     uint64_t peers = __ballot(valid);
     for (int bit = 0; bit < id_bits; ++bit) {
@@ -121,20 +154,15 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
       peers &= set ? m : ~m;
     }
     const int rank = __popcll(peers & lt_mask);
-    const int wcount = __popcll(peers);
-    if (valid && rank == 0) s_wcnt[wave][e] = (uint8_t)wcount;
-    __syncthreads();
+    const int count = __popcll(peers);
+    int slot = 0;
+    if (valid) slot = s_wcnt[wave][e] + rank;
+    __builtin_amdgcn_wave_barrier();
     if (valid) {
-      int before = 0;
-      for (int w = 0; w < wave; ++w) before += s_wcnt[w][e];
-      sorted_ids[s_boff[e] * BM + s_cur[e] + before + rank] = i;
+      sorted_ids[slot] = i;
+      if (rank == 0) s_wcnt[wave][e] = slot + count;
     }
-    __syncthreads();
-    if (valid && rank == 0) {
-      atomicAdd(&s_cur[e], wcount);
-      s_wcnt[wave][e] = 0;
-    }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
