@@ -103,6 +103,49 @@ __device__ __forceinline__ void load_scale_run(__amdgpu_buffer_rsrc_t r, uint32_
   }
 }
 
+// ---- LDS layout of the staged activations ---------------------------------
+// ds_read_b128 / ds_write_b128 are served 32 lanes per cycle across 128
+// four-byte banks, i.e. 32 sixteen-byte segments: a cycle is conflict-free
+// when its 32 lanes touch 32 distinct segments (mod 32).
+//
+// Rows are PITCH = KC + 32 bytes apart, so PITCH / 16 = 2 * odd and the 16
+// rows of an MFMA A fragment start on 16 distinct even segments. Within a
+// K-group, the 16-byte unit that K slot kb of MFMA step s reads (K-order unit
+// kb * S + s) is stored at position 4 * s + kb; lanes 0-31 (kb = 0, 1) then
+// read 32 distinct segments for every s.
+//
+// Stores: a 32-lane half writes 32 / UPR rows (UPR 16-byte units per row).
+// Rows r and r + XD, with (PITCH / 16) * XD = UPR (mod 32), land on disjoint
+// segment ranges, so each half writes such rows: row_of_group() maps the
+// q-th row group of the thread order to a row, bijectively within every 16
+// rows.
+__host__ __device__ constexpr int lds_row_step(int upr) {
+  int d = 1;
+  while (d < 32 && ((upr + 2) * d) % 32 != upr % 32) ++d;
+  return d;
+}
+
+template <int UPR>
+__device__ __forceinline__ int row_of_group(int q) {
+  if constexpr (UPR >= 32) {
+    return q;
+  } else {
+    constexpr int XR = 32 / UPR;            // rows per 32-lane half
+    constexpr int XD = lds_row_step(UPR);   // row distance within a half
+    static_assert(XR * XD == 16, "row interleave must tile 16 rows");
+    const int j = q % XR, b = q / XR;
+    return (b % XD) + XD * j + 16 * (b / XD);
+  }
+}
+
+// LDS byte position of K-order unit cu (16 bytes) within a row's chunk.
+template <int GS>
+__device__ __forceinline__ int unit_pos(int cu) {
+  constexpr int S = GS / 64, UG = GS / 16;
+  const int g = cu / UG, v = cu - g * UG;
+  return 16 * (g * UG + (v % S) * 4 + v / S);
+}
+
 // Per-tile values shared by the kernel's setup and its tile bodies.
 struct TileCtx {
   int e;          // expert
@@ -132,7 +175,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   constexpr int S = GS / 64;          // MFMA K-steps per group
   constexpr int WD = 2 * S;           // packed dwords per lane per (group, column block)
   constexpr int KC = KCG * GS;        // activation bytes per row per chunk
-  constexpr int PITCH = KC + 16;      // LDS row pitch in bytes
+  constexpr int PITCH = KC + 32;      // LDS row pitch in bytes (see the layout note)
   constexpr int BUF = BM * PITCH;     // bytes per LDS buffer
   constexpr int UPR = KC / 16;        // 16-byte units per row and chunk
   constexpr int XU = (BMX * UPR + NT - 1) / NT;
@@ -164,14 +207,19 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   }
   // only rows that hold data are staged; padding rows stay whatever LDS holds
   // and their results are never stored
-  const int xunits = min(c.rows, BMX) * UPR;
+  const int vrows = min(c.rows, BMX);
   uint32_t x_off[XU];
+  int x_lds[XU];   // LDS byte offset within a buffer, -1 when not staged
 #pragma unroll
   for (int j = 0; j < XU; ++j) {
     const int u = tid + j * NT;
-    const int row = min(u / UPR, BMX - 1);
-    const int src = s_src[row];
-    x_off[j] = src >= 0 ? (uint32_t)(src * a.ldx) + (uint32_t)((u - (u / UPR) * UPR) * 16) : kOOB;
+    const int q = u / UPR;
+    const int cu = u - q * UPR;
+    const int row = row_of_group<UPR>(q);
+    const bool ok = u < BMX * UPR && row < vrows;
+    const int src = s_src[ok ? row : 0];
+    x_off[j] = ok && src >= 0 ? (uint32_t)(src * a.ldx) + (uint32_t)(cu * 16) : kOOB;
+    x_lds[j] = ok ? row * PITCH + unit_pos<GS>(cu) : -1;
   }
 
   // ---- the tile's zero points and scales -> registers (ZS_LDS) -------------
@@ -206,23 +254,20 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   auto load_x = [&](int ch) {
 #pragma unroll
     for (int j = 0; j < XU; ++j)
-      if (tid + j * NT < xunits)
+      if (x_lds[j] >= 0)
         xr[j] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, x_off[j] + (uint32_t)(ch * KC), 0, 0);
   };
   auto store_x = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < XU; ++j) {
-      const int u = tid + j * NT;
-      if (u < xunits) {
-        const int row = u / UPR;
-        const int cu = u - row * UPR;
+      if (x_lds[j] >= 0) {
         const u32x4 v = xr[j];
         u32x4 p;
         p.x = even_bytes(v.x, v.y);
         p.y = odd_bytes(v.x, v.y);
         p.z = even_bytes(v.z, v.w);
         p.w = odd_bytes(v.z, v.w);
-        *reinterpret_cast<u32x4*>(s_x + buf * BUF + row * PITCH + cu * 16) = p;
+        *reinterpret_cast<u32x4*>(s_x + buf * BUF + x_lds[j]) = p;
       }
     }
   };
@@ -299,17 +344,46 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
           }
         }
         i32x4 bfr[NB][S];
+        // Symmetric int4 (every zero point of this group in the wave is 8):
+        // 16 * (u - 8) is the nibble with its top bit flipped, moved into the
+        // high half of its byte, so unpacking takes 2 ops per int8 dword
+        // instead of 3.5. The partials come out 16x larger and the scale is
+        // used / 16; both factors are powers of two and the product fed to
+        // the FMA is the same real number, so the result is bit-identical.
+        bool sym = false;
+        if constexpr (!DEBUGP) {
+          bool z8 = true;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const ZeroFold zf = make_zero_fold(zv[nb]);
+          for (int nb = 0; nb < NB; ++nb) z8 = z8 && zv[nb] == 8;
+          sym = __all(z8);
+        }
+        if (sym) {
 #pragma unroll
-          for (int s = 0; s < S; ++s) {
-            const uint32_t d0 = wc.w[g][nb][2 * s];
-            const uint32_t d1 = wc.w[g][nb][2 * s + 1];
-            bfr[nb][s].x = (int)fold_even(d0, zf);
-            bfr[nb][s].y = (int)fold_odd(d0, zf);
-            bfr[nb][s].z = (int)fold_even(d1, zf);
-            bfr[nb][s].w = (int)fold_odd(d1, zf);
+          for (int nb = 0; nb < NB; ++nb) {
+            sv[nb] *= 0.0625f;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+              const uint32_t t0 = wc.w[g][nb][2 * s] ^ 0x88888888u;
+              const uint32_t t1 = wc.w[g][nb][2 * s + 1] ^ 0x88888888u;
+              bfr[nb][s].x = (int)((t0 << 4) & 0xF0F0F0F0u);
+              bfr[nb][s].y = (int)(t0 & 0xF0F0F0F0u);
+              bfr[nb][s].z = (int)((t1 << 4) & 0xF0F0F0F0u);
+              bfr[nb][s].w = (int)(t1 & 0xF0F0F0F0u);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const ZeroFold zf = make_zero_fold(zv[nb]);
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+              const uint32_t d0 = wc.w[g][nb][2 * s];
+              const uint32_t d1 = wc.w[g][nb][2 * s + 1];
+              bfr[nb][s].x = (int)fold_even(d0, zf);
+              bfr[nb][s].y = (int)fold_odd(d0, zf);
+              bfr[nb][s].z = (int)fold_even(d1, zf);
+              bfr[nb][s].w = (int)fold_odd(d1, zf);
+            }
           }
         }
         // Software-pipelined over 16-row blocks: the A fragments of block
@@ -317,10 +391,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         // int32 partials are folded into the fp32 accumulators after block
         // mb's MFMAs are issued, so neither the LDS latency nor the MFMA
         // result latency sits on the issue path.
-        const int8_t* xg = xb + jl * PITCH + g * GS + kb * (GS / 4);
+        const int8_t* xg = xb + jl * PITCH + g * GS + kb * 16;
         auto read_a = [&](int mb, i32x4 (&av)[S]) {
 #pragma unroll
-          for (int s = 0; s < S; ++s) av[s] = *reinterpret_cast<const i32x4*>(xg + mb * 16 * PITCH + 16 * s);
+          for (int s = 0; s < S; ++s) av[s] = *reinterpret_cast<const i32x4*>(xg + mb * 16 * PITCH + 64 * s);
         };
         auto fold = [&](int mb, const i32x4 (&part)[NB]) {
           if constexpr (DEBUGP) {
@@ -420,7 +494,7 @@ template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, bool ROUTED,
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU)))
 void w4a8_gemm_kernel(const GemmArgs a) {
   constexpr int BN = NW * WN;
-  constexpr int PITCH = KCG * GS + 16;
+  constexpr int PITCH = KCG * GS + 32;
   constexpr bool ZS_LDS = ZSG > 0;
   static_assert(BM % 16 == 0 && WN % 16 == 0 && GS % 64 == 0, "tile shape");
 

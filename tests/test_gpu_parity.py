@@ -134,6 +134,20 @@ def test_grouped_edge_cases(pkg, dev):
     assert_close(out, ref, 512, "edge/strided x")
 
 
+@pytest.mark.parametrize("gs", [64, 128, 256])
+def test_grouped_mixed_symmetric_groups(pkg, dev, gs):
+    """Zero points equal to 8 take the symmetric unpacking; groups or single
+    columns with other zero points take the general one, group by group."""
+    wl = pkg.workloads
+    x_q, x_scale, w_q4, w_scale, w_zero, offs = wl.make_grouped_inputs(3, 150, 384, 1024, gs, seed=83,
+                                                                       zero="symmetric")
+    w_zero[:, :, 1::3] = 5          # whole groups off the fast path
+    w_zero[0, 7, 0] = 9             # one column of one wave
+    w_zero[2, 200:216, -1] = -120   # a 16-column block in the wrap regime
+    out, ref = _run_grouped(pkg, dev, x_q, x_scale, w_q4, w_scale, w_zero, offs, gs)
+    assert_close(out, ref, 384, f"mixed symmetric gs={gs}")
+
+
 @pytest.mark.parametrize("case", ["misaligned", "many_groups"])
 def test_grouped_scale_zero_fallback_paths(pkg, dev, case):
     """Zero points/scales that cannot use the tile-block LDS copy (a group
