@@ -205,21 +205,21 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     w_off[nb] = ok ? (uint32_t)col * khalf + (uint32_t)(kb * (GS / 8)) : kOOB;
     zs_off[nb] = ok ? (uint32_t)(col * a.G) : kOOB;
   }
-  // only rows that hold data are staged; padding rows stay whatever LDS holds
-  // and their results are never stored
-  const int vrows = min(c.rows, BMX);
+  // Padding rows read zeros (out-of-range offset) and are staged like the
+  // others, which keeps the staging loops free of per-lane branches; their
+  // results are never stored.
+  static_assert((BMX * UPR) % NT == 0, "staging units must divide evenly over the threads");
   uint32_t x_off[XU];
-  int x_lds[XU];   // LDS byte offset within a buffer, -1 when not staged
+  int x_lds[XU];   // LDS byte offset within a buffer
 #pragma unroll
   for (int j = 0; j < XU; ++j) {
     const int u = tid + j * NT;
     const int q = u / UPR;
     const int cu = u - q * UPR;
     const int row = row_of_group<UPR>(q);
-    const bool ok = u < BMX * UPR && row < vrows;
-    const int src = s_src[ok ? row : 0];
-    x_off[j] = ok && src >= 0 ? (uint32_t)(src * a.ldx) + (uint32_t)(cu * 16) : kOOB;
-    x_lds[j] = ok ? row * PITCH + unit_pos<GS>(cu) : -1;
+    const int src = s_src[row];
+    x_off[j] = src >= 0 ? (uint32_t)(src * a.ldx) + (uint32_t)(cu * 16) : kOOB;
+    x_lds[j] = row * PITCH + unit_pos<GS>(cu);
   }
 
   // ---- the tile's zero points and scales -> registers (ZS_LDS) -------------
@@ -254,21 +254,18 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   auto load_x = [&](int ch) {
 #pragma unroll
     for (int j = 0; j < XU; ++j)
-      if (x_lds[j] >= 0)
-        xr[j] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, x_off[j] + (uint32_t)(ch * KC), 0, 0);
+      xr[j] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, x_off[j] + (uint32_t)(ch * KC), 0, 0);
   };
   auto store_x = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < XU; ++j) {
-      if (x_lds[j] >= 0) {
-        const u32x4 v = xr[j];
-        u32x4 p;
-        p.x = even_bytes(v.x, v.y);
-        p.y = odd_bytes(v.x, v.y);
-        p.z = even_bytes(v.z, v.w);
-        p.w = odd_bytes(v.z, v.w);
-        *reinterpret_cast<u32x4*>(s_x + buf * BUF + x_lds[j]) = p;
-      }
+      const u32x4 v = xr[j];
+      u32x4 p;
+      p.x = even_bytes(v.x, v.y);
+      p.y = odd_bytes(v.x, v.y);
+      p.z = even_bytes(v.z, v.w);
+      p.w = odd_bytes(v.z, v.w);
+      *reinterpret_cast<u32x4*>(s_x + buf * BUF + x_lds[j]) = p;
     }
   };
 
