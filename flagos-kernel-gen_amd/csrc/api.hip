@@ -230,13 +230,9 @@ int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const 
   rc = mw4a8_align_sizes((int)pairs, E, block_m, &sorted_len, &blocks_len);
   if (rc) return rc;
   a.sorted_len = sorted_len;
-  const int ne = E < (int)pairs ? E : (int)pairs;
-  TileConfig cfg = select_tiles((int)pairs, ne, N, K, group_size);
-  // the routing metadata fixes the row block; keep the rest of the choice
-  if (cfg.BM != block_m) {
-    const TileConfig forced = select_tiles(block_m * ne, ne, N, K, group_size);
-    cfg = forced;
-  }
+  // the routing metadata fixes the row block
+  const TileConfig cfg = tiles_for_block_m(block_m, group_size);
+  if (cfg.BM != block_m) return fail(MW4A8_ERR_UNSUPPORTED, "block_m must be 16, 32, 64 or 128");
   const int max_blocks = max_row_blocks((int)pairs, E, block_m);
   hipError_t e = launch_grouped_gemm(a, cfg, group_size, true, max_blocks, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "fused MoE launch");

@@ -633,7 +633,7 @@ static hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, h
     case 32:
       if (zs_block_fits(a, 64, 64)) return launch_one<32, 16, 4, GS, K512, 2, 64, ROUTED, false, 1>(a, max_blocks, c.R, s);
       return launch_one<32, 16, 4, GS, K512, 2, 0, ROUTED, false, 1>(a, max_blocks, c.R, s);
-    case 64: return launch_one<64, 32, 4, GS, K256, 2, 0, ROUTED, false, 2>(a, max_blocks, c.R, s);
+    case 64: return launch_one<64, 32, 4, GS, K256, 2, 0, ROUTED, false, 3>(a, max_blocks, c.R, s);
     case 128: return launch_one<128, 32, 4, GS, K256, 2, 0, ROUTED, false, 2>(a, max_blocks, c.R, s);
     default: return hipErrorInvalidValue;
   }
@@ -664,24 +664,30 @@ int max_row_blocks(int rows, int experts, int BM) {
   return (int)(bound < rows ? bound : rows);
 }
 
-TileConfig select_tiles(int rows, int touched_experts, int N, int K, int group_size) {
-  (void)N;
-  (void)K;
-  (void)group_size;
-  const int ne = touched_experts < 1 ? 1 : touched_experts;
-  const int per_expert = (rows + ne - 1) / ne;
+TileConfig tiles_for_block_m(int BM, int group_size) {
   TileConfig c;
   c.NW = 4;
-  if (per_expert <= 16) {
-    c.BM = 16; c.WN = 16; c.KCG = 1024 / group_size; c.R = 1;
-  } else if (per_expert <= 32) {
-    c.BM = 32; c.WN = 16; c.KCG = 512 / group_size; c.R = 1;
-  } else if (per_expert <= 64) {
-    c.BM = 64; c.WN = 32; c.KCG = 256 / group_size; c.R = 2;
-  } else {
-    c.BM = 128; c.WN = 32; c.KCG = 256 / group_size; c.R = 2;
+  c.BM = BM;
+  switch (BM) {
+    case 16: c.WN = 16; c.KCG = 1024 / group_size; c.R = 1; break;
+    case 32: c.WN = 16; c.KCG = 512 / group_size; c.R = 1; break;
+    case 64: c.WN = 32; c.KCG = 256 / group_size; c.R = 2; break;
+    default: c.BM = 128; c.WN = 32; c.KCG = 256 / group_size; c.R = 2; break;
   }
+  if (c.KCG < 1) c.KCG = 1;
   return c;
+}
+
+TileConfig select_tiles(int rows, int touched_experts, int N, int K, int group_size) {
+  (void)N;
+  const int ne = touched_experts < 1 ? 1 : touched_experts;
+  const int per_expert = (rows + ne - 1) / ne;
+  if (per_expert <= 16) return tiles_for_block_m(16, group_size);
+  if (per_expert <= 32) return tiles_for_block_m(32, group_size);
+  // 128-row tiles pay off only over a long K loop (measured on MI355X:
+  // K = 7168 prefers 128 rows, K = 2048 prefers 64)
+  if (per_expert <= 64 || K < 4096) return tiles_for_block_m(64, group_size);
+  return tiles_for_block_m(128, group_size);
 }
 
 }  // namespace mw4a8

@@ -50,6 +50,9 @@ struct TileConfig {
 // Tile choice by expected rows per touched expert (no device sync).
 TileConfig select_tiles(int rows, int touched_experts, int N, int K, int group_size);
 
+// The tile configuration of row-block size BM (16, 32, 64 or 128).
+TileConfig tiles_for_block_m(int BM, int group_size);
+
 // Upper bound on the number of row blocks for `rows` rows spread over at
 // most `experts` experts: every expert adds at most one partial block.
 int max_row_blocks(int rows, int experts, int BM);

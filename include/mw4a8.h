@@ -82,7 +82,8 @@ int mw4a8_align_sizes(int num_pairs, int E, int block_m, int* sorted_len, int* b
 
 /*
  * Row-block size the library would pick for a routed problem (16, 32, 64
- * or 128), chosen from the expected rows per touched expert. Mirrors the
+ * or 128), chosen from the expected rows per touched expert and, above 64
+ * rows, from K (128-row blocks only for K >= 4096). Mirrors the
  * reference's block-M heuristic (Task1/v1.6/task1-codex5.5-all-v1.6.py:648-653)
  * without its device->host read of the per-expert maximum (:62-64).
  */

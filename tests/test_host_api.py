@@ -45,6 +45,9 @@ def test_sizes_and_tile_selection(pkg):
     assert pkg.select_block_m(32768, 256, 4096, 7168, 128) == 128
     assert pkg.select_block_m(512, 256, 4096, 7168, 128) == 16
     assert pkg.select_block_m(64 * 8, 8, 2048, 1024, 128) == 64
+    # long expert row lists: 128-row tiles for a long K loop, 64 for a short one
+    assert pkg.select_block_m(32768, 256, 7168, 2048, 128) == 64
+    assert pkg.select_block_m(16384, 128, 1536, 2048, 128) == 64
 
 
 def test_c_abi_rejects_bad_arguments_without_device_work(pkg):
