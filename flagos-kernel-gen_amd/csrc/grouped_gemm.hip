@@ -633,7 +633,8 @@ static hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, h
     case 32:
       if (zs_block_fits(a, 64, 64)) return launch_one<32, 16, 4, GS, K512, 2, 64, ROUTED, false, 1>(a, max_blocks, c.R, s);
       return launch_one<32, 16, 4, GS, K512, 2, 0, ROUTED, false, 1>(a, max_blocks, c.R, s);
-    case 64: return launch_one<64, 32, 4, GS, K256, 2, 0, ROUTED, false, 3>(a, max_blocks, c.R, s);
+    // three waves per SIMD fit the gs = 128 body without spills; the others keep two
+    case 64: return launch_one<64, 32, 4, GS, K256, 2, 0, ROUTED, false, GS == 128 ? 3 : 2>(a, max_blocks, c.R, s);
     case 128: return launch_one<128, 32, 4, GS, K256, 2, 0, ROUTED, false, 2>(a, max_blocks, c.R, s);
     default: return hipErrorInvalidValue;
   }

@@ -134,6 +134,19 @@ def test_grouped_edge_cases(pkg, dev):
     assert_close(out, ref, 512, "edge/strided x")
 
 
+@pytest.mark.parametrize("K,rows", [(1152, 300), (1280, 300), (1152, 40), (4224, 1000)])
+def test_grouped_partial_chunks(pkg, dev, K, rows):
+    """K-group counts that leave a partial last chunk (G = 9, 33) or an odd
+    number of chunks (G = 10) take the guarded loop; 40 rows per call use the
+    small-tile decode kernels, 300 rows the 64-row tiles and 1000 rows over
+    K = 4224 the 128-row ones."""
+    wl = pkg.workloads
+    print(f"[partial] K={K} rows={rows}", flush=True)
+    x_q, x_scale, w_q4, w_scale, w_zero, offs = wl.make_grouped_inputs(2, rows, 256, K, 128, seed=K + rows)
+    out, ref = _run_grouped(pkg, dev, x_q, x_scale, w_q4, w_scale, w_zero, offs, 128)
+    assert_close(out, ref, 256, f"partial chunks K={K} rows={rows}")
+
+
 @pytest.mark.parametrize("gs", [64, 128, 256])
 def test_grouped_mixed_symmetric_groups(pkg, dev, gs):
     """Zero points equal to 8 take the symmetric unpacking; groups or single
