@@ -164,7 +164,12 @@ struct TileCtx {
 //     (G <= ZSG) is copied into LDS once -- it is contiguous in memory -- so
 //     the K loop issues no loads for them. When zero they travel with the
 //     weights, one vector run per column and chunk when aligned.
-template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, bool ROUTED, bool DEBUGP>
+// FAST: the host guarantees that every chunk is full and the chunk count is
+//     a multiple of RD (G % (KCG * RD) == 0) and, without ZSG, that the
+//     zero-point / scale runs are aligned; the loop then carries no guards.
+//     (Used for the 16- and 32-row tiles only: without the guards the
+//     compiler schedules the larger bodies into scratch.)
+template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, bool ROUTED, bool DEBUGP, bool FAST>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, int8_t* s_x, float* s_scale,
                                           int8_t* s_zero, const int* s_src, const int* s_dst, const float* s_xs,
                                           const float* s_tw) {
@@ -295,14 +300,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
             d.w[g][nb][4 * h + 3] = q.w;
           }
         }
-        if (!ZS_LDS && !a.zs_vec) {
+        if (!ZS_LDS && !FAST && !a.zs_vec) {
           d.z[g][nb] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(z_rsrc, zs_off[nb] + gg, 0, 0);
           if constexpr (!DEBUGP)
             d.s[g][nb] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(s_rsrc, (zs_off[nb] + gg) * 4u, 0, 0));
         }
       }
     }
-    if (!ZS_LDS && a.zs_vec) {
+    if (!ZS_LDS && (FAST || a.zs_vec)) {
       // the chunk's KCG zero points and scales of a column are contiguous:
       // one or two vector loads per column instead of 2 * KCG scalar loads
 #pragma unroll
@@ -327,7 +332,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 #pragma unroll
     for (int g = 0; g < KCG; ++g) {
       const int gg = ch * KCG + g;
-      if (gg < a.G) {
+      if (FAST || gg < a.G) {
         int zv[NB];
         float sv[NB];
 #pragma unroll
@@ -455,7 +460,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 #pragma unroll
     for (int d = 0; d < RD; ++d) {
       const int cc = ch + d;
-      if (cc < c.nchunks) {
+      if (FAST || cc < c.nchunks) {
         store_x(cc & 1);
         __syncthreads();
         if (cc + 1 < c.nchunks) load_x(cc + 1);
@@ -487,7 +492,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 
 // ZSG > 0: zero points and scales come from an LDS copy of the tile's
 // block; the host launches this only when G <= ZSG (see zs_block_fits).
-template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, bool ROUTED, bool DEBUGP, int WAVES_PER_EU>
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, bool ROUTED, bool DEBUGP, bool FAST,
+          int WAVES_PER_EU>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU)))
 void w4a8_gemm_kernel(const GemmArgs a) {
   constexpr int BN = NW * WN;
@@ -577,12 +583,12 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   // tiles whose valid rows fit in the top half run the half-height body
   if constexpr (BM >= 64) {
     if (rows <= BM / 2) {
-      gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP>(a, c, s_x, s_scale, s_zero, s_src, s_dst,
+      gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP, FAST>(a, c, s_x, s_scale, s_zero, s_src, s_dst,
                                                                      s_xs, s_tw);
       return;
     }
   }
-  gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP>(a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs, s_tw);
+  gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP, FAST>(a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs, s_tw);
 }
 
 // ---------------------------------------------------------------------------
@@ -611,8 +617,15 @@ static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   a.zs_vec = (a.G % KCG == 0) && (reinterpret_cast<uintptr_t>(a.wz) % 16 == 0) &&
              (reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
   if (a.total_tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP, WPE>), dim3(8 * a.per_xcd),
-                     dim3(NW * 64), 0, s, a);
+  // the guard-free body needs whole chunks, a chunk count divisible by the
+  // unroll, and (without the LDS zero/scale block) aligned vector runs
+  constexpr bool CAN_FAST = !DEBUGP && BM <= 32;
+  if (CAN_FAST && a.G % (KCG * RD) == 0 && (ZSG > 0 || a.zs_vec))
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP, CAN_FAST, WPE>),
+                       dim3(8 * a.per_xcd), dim3(NW * 64), 0, s, a);
+  else
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP, false, WPE>),
+                       dim3(8 * a.per_xcd), dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
 
