@@ -20,7 +20,7 @@ LIB_NAME = "libmw4a8.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 ARCH = "gfx950"
 
-SOURCES = ("api.hip", "moe_align.hip", "grouped_gemm.hip")
+SOURCES = ("api.hip", "moe_align.hip", "grouped_gemm.hip", "moe_layer.hip")
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

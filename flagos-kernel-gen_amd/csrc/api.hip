@@ -210,8 +210,7 @@ int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const 
   int rc = check_gemm_args(x_q, ldx, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, M, N, K, E, group_size,
                            true);
   if (rc) return rc;
-  if (!sorted_ids || !expert_ids || !num_post_pad || !topk_weights)
-    return fail(MW4A8_ERR_INVALID, "null routing pointer");
+  if (!sorted_ids || !expert_ids || !num_post_pad) return fail(MW4A8_ERR_INVALID, "null routing pointer");
   if (!aligned(topk_weights, 4)) return fail(MW4A8_ERR_INVALID, "misaligned topk_weights");
   if (block_m != 16 && block_m != 32 && block_m != 64 && block_m != 128)
     return fail(MW4A8_ERR_UNSUPPORTED, "block_m=%d not in {16,32,64,128}", block_m);
@@ -236,6 +235,75 @@ int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const 
   const int max_blocks = max_row_blocks((int)pairs, E, block_m);
   hipError_t e = launch_grouped_gemm(a, cfg, group_size, true, max_blocks, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "fused MoE launch");
+  return MW4A8_OK;
+}
+
+// ---------------------------------------------------------------------------
+// MoE-layer kernels around the GEMM
+
+int mw4a8_quant_rows(const uint16_t* x_bf16, int64_t ldx, int M, int K, int8_t* x_q, int64_t ldq, float* x_scale,
+                     void* stream) {
+  g_err[0] = 0;
+  if (M < 0 || K <= 0) return fail(MW4A8_ERR_INVALID, "bad sizes: M=%d K=%d", M, K);
+  if (M == 0) return MW4A8_OK;
+  if (!x_bf16 || !x_q || !x_scale) return fail(MW4A8_ERR_INVALID, "null tensor pointer");
+  if (K % 8 != 0 || ldx < K || ldq < K || ldx % 8 != 0 || ldq % 8 != 0)
+    return fail(MW4A8_ERR_INVALID, "K=%d, ldx=%lld, ldq=%lld must be multiples of 8 with ld >= K", K,
+                (long long)ldx, (long long)ldq);
+  if (!aligned(x_bf16, 16) || !aligned(x_q, 8) || !aligned(x_scale, 4))
+    return fail(MW4A8_ERR_INVALID, "x must be 16-byte, x_q 8-byte aligned");
+  hipError_t e = launch_quant_rows(x_bf16, ldx, M, K, x_q, ldq, x_scale, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "quant_rows launch");
+  return MW4A8_OK;
+}
+
+int mw4a8_router_topk(const float* logits, int64_t ld, int M, int E, int topk, int renormalize, int32_t* topk_ids,
+                      float* topk_weights, void* stream) {
+  g_err[0] = 0;
+  if (M < 0 || E <= 0 || topk <= 0 || ld < E) return fail(MW4A8_ERR_INVALID, "bad sizes: M=%d E=%d topk=%d", M, E, topk);
+  if (E > 1024 || topk > 64 || topk > E)
+    return fail(MW4A8_ERR_UNSUPPORTED, "router supports E <= 1024 and topk <= min(E, 64)");
+  if (M == 0) return MW4A8_OK;
+  if (!logits || !topk_ids || !topk_weights) return fail(MW4A8_ERR_INVALID, "null tensor pointer");
+  if (!aligned(logits, 4) || !aligned(topk_ids, 4) || !aligned(topk_weights, 4))
+    return fail(MW4A8_ERR_INVALID, "misaligned router pointer");
+  hipError_t e = launch_router_topk(logits, ld, M, E, topk, renormalize ? 1 : 0, topk_ids, topk_weights,
+                                    static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "router_topk launch");
+  return MW4A8_OK;
+}
+
+int mw4a8_silu_mul_quant(const uint16_t* h_bf16, int64_t ldh, int P, int I, int8_t* q, int64_t ldq, float* scale,
+                         void* stream) {
+  g_err[0] = 0;
+  if (P < 0 || I <= 0) return fail(MW4A8_ERR_INVALID, "bad sizes: P=%d I=%d", P, I);
+  if (P == 0) return MW4A8_OK;
+  if (!h_bf16 || !q || !scale) return fail(MW4A8_ERR_INVALID, "null tensor pointer");
+  if (I % 8 != 0 || ldh < 2 * (int64_t)I || ldq < I || ldh % 8 != 0 || ldq % 8 != 0)
+    return fail(MW4A8_ERR_INVALID, "I=%d, ldh=%lld, ldq=%lld: need I %% 8 == 0, ldh >= 2I, ldq >= I, both %% 8 == 0",
+                I, (long long)ldh, (long long)ldq);
+  if (!aligned(h_bf16, 16) || !aligned(q, 8) || !aligned(scale, 4))
+    return fail(MW4A8_ERR_INVALID, "h must be 16-byte, q 8-byte aligned");
+  hipError_t e = launch_silu_mul_quant(h_bf16, ldh, P, I, q, ldq, scale, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "silu_mul_quant launch");
+  return MW4A8_OK;
+}
+
+int mw4a8_combine_topk(const uint16_t* y_bf16, int64_t ldy, int M, int topk, int N, const float* topk_weights,
+                       uint16_t* out_bf16, int64_t ldo, void* stream) {
+  g_err[0] = 0;
+  if (M < 0 || topk <= 0 || N <= 0) return fail(MW4A8_ERR_INVALID, "bad sizes: M=%d topk=%d N=%d", M, topk, N);
+  if (M == 0) return MW4A8_OK;
+  if (!y_bf16 || !out_bf16) return fail(MW4A8_ERR_INVALID, "null tensor pointer");
+  if (N % 8 != 0 || ldy < N || ldo < N || ldy % 8 != 0 || ldo % 8 != 0)
+    return fail(MW4A8_ERR_INVALID, "N=%d, ldy=%lld, ldo=%lld must be multiples of 8 with ld >= N", N,
+                (long long)ldy, (long long)ldo);
+  if (!aligned(y_bf16, 16) || !aligned(out_bf16, 16) || !aligned(topk_weights, 4))
+    return fail(MW4A8_ERR_INVALID, "y and out must be 16-byte aligned");
+  if ((int64_t)M * topk > 0x7fffffff) return fail(MW4A8_ERR_UNSUPPORTED, "too many rows");
+  hipError_t e = launch_combine_topk(y_bf16, ldy, M, topk, N, topk_weights, out_bf16, ldo,
+                                     static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "combine_topk launch");
   return MW4A8_OK;
 }
 

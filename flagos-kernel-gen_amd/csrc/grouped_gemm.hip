@@ -556,7 +556,7 @@ void w4a8_gemm_kernel(const GemmArgs a) {
         src = s / a.topk;
         dst = s;
         xsv = a.xs[src];
-        twv = a.tw[s];
+        twv = a.tw ? a.tw[s] : 1.f;
       }
     } else {
       const int r = a.blk_row0[b] + tid;

@@ -1,0 +1,283 @@
+// Kernels around the grouped GEMM that complete a W4A8 MoE layer:
+//
+//   quant_rows      bf16 activations -> per-token int8 + fp32 scale (the
+//                   producer of the GEMM's x_q / x_scale)
+//   router_topk     router logits -> top-k expert ids + routing weights
+//   silu_mul_quant  up/gate GEMM output [gate | up] -> int8 silu(gate)*up +
+//                   per-row scale (the down GEMM's activations); the math of
+//                   the forward half of reference docs/Task3.md:103-110
+//   combine_topk    per-pair down-projection rows -> per-token sum
+//
+// All four are HBM-bound streaming kernels. Rows are handled by one
+// workgroup (quant kernels) or one wave (router) so that reductions stay on
+// chip; vector accesses move 16 bytes per lane.
+#include "mw4a8_internal.h"
+#include "mw4a8_pack.h"
+
+namespace mw4a8 {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+namespace {
+
+constexpr int kRowThreads = 256;
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// 8 bf16 values packed in a 16-byte vector -> fp32
+__device__ __forceinline__ void unpack8(const u32x4 v, float (&f)[8]) {
+  f[0] = __uint_as_float(v.x << 16);
+  f[1] = __uint_as_float(v.x & 0xffff0000u);
+  f[2] = __uint_as_float(v.y << 16);
+  f[3] = __uint_as_float(v.y & 0xffff0000u);
+  f[4] = __uint_as_float(v.z << 16);
+  f[5] = __uint_as_float(v.z & 0xffff0000u);
+  f[6] = __uint_as_float(v.w << 16);
+  f[7] = __uint_as_float(v.w & 0xffff0000u);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// max over the workgroup (kRowThreads threads); every thread gets the result
+__device__ __forceinline__ float block_max(float v, float* s_red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();   // s_red may still be read by a previous call
+  if (lane == 0) s_red[wave] = v;
+  __syncthreads();
+  float m = s_red[0];
+#pragma unroll
+  for (int w = 1; w < kRowThreads / 64; ++w) m = fmaxf(m, s_red[w]);
+  return m;
+}
+
+// Per-token symmetric int8: scale = max(amax, 1e-12) / 127,
+// q = clamp(round_half_even(v / scale), -127, 127). IEEE division and
+// rint() make it bit-identical to the same float32 steps on the CPU.
+__device__ __forceinline__ float row_scale(float amax) { return fmaxf(amax, 1e-12f) / 127.0f; }
+
+__device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, float scale) {
+  const int qa = (int)fminf(fmaxf(rintf(a / scale), -127.f), 127.f);
+  const int qb = (int)fminf(fmaxf(rintf(b / scale), -127.f), 127.f);
+  const int qc = (int)fminf(fmaxf(rintf(c / scale), -127.f), 127.f);
+  const int qd = (int)fminf(fmaxf(rintf(d / scale), -127.f), 127.f);
+  return (uint32_t)(qa & 0xff) | ((uint32_t)(qb & 0xff) << 8) | ((uint32_t)(qc & 0xff) << 16) |
+         ((uint32_t)(qd & 0xff) << 24);
+}
+
+// One workgroup per row; K % 8 == 0, rows 16-byte aligned (checked on the host).
+__global__ __launch_bounds__(kRowThreads) void quant_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                 int K, int8_t* __restrict__ q, int64_t ldq,
+                                                                 float* __restrict__ scale) {
+  __shared__ float s_red[kRowThreads / 64];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * ldx;
+  float amax = 0.f;
+  for (int c = threadIdx.x * 8; c < K; c += kRowThreads * 8) {
+    float f[8];
+    unpack8(*reinterpret_cast<const u32x4*>(xr + c), f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
+  }
+  const float s = row_scale(block_max(amax, s_red));
+  int8_t* qr = q + row * ldq;
+  for (int c = threadIdx.x * 8; c < K; c += kRowThreads * 8) {
+    float f[8];
+    unpack8(*reinterpret_cast<const u32x4*>(xr + c), f);
+    u32x2 o;
+    o.x = quant4(f[0], f[1], f[2], f[3], s);
+    o.y = quant4(f[4], f[5], f[6], f[7], s);
+    *reinterpret_cast<u32x2*>(qr + c) = o;
+  }
+  if (threadIdx.x == 0) scale[row] = s;
+}
+
+// y = silu(gate) * up in fp32 as sigmoid = 1 / (1 + exp(-g)), silu = g *
+// sigmoid, y = silu * up (reference docs/Task3.md:103-110 order).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float sg = 1.0f / (1.0f + expf(-g));
+  return (g * sg) * u;
+}
+
+// One workgroup per row of h = [gate (I) | up (I)] bf16; I % 8 == 0.
+__global__ __launch_bounds__(kRowThreads) void silu_mul_quant_kernel(const uint16_t* __restrict__ h,
+                                                                     int64_t ldh, int I, int8_t* __restrict__ q,
+                                                                     int64_t ldq, float* __restrict__ scale) {
+  __shared__ float s_red[kRowThreads / 64];
+  const int64_t row = blockIdx.x;
+  const uint16_t* hr = h + row * ldh;
+  float amax = 0.f;
+  for (int c = threadIdx.x * 8; c < I; c += kRowThreads * 8) {
+    float g[8], u[8];
+    unpack8(*reinterpret_cast<const u32x4*>(hr + c), g);
+    unpack8(*reinterpret_cast<const u32x4*>(hr + I + c), u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(silu_mul(g[i], u[i])));
+  }
+  const float s = row_scale(block_max(amax, s_red));
+  int8_t* qr = q + row * ldq;
+  for (int c = threadIdx.x * 8; c < I; c += kRowThreads * 8) {
+    float g[8], u[8], y[8];
+    unpack8(*reinterpret_cast<const u32x4*>(hr + c), g);
+    unpack8(*reinterpret_cast<const u32x4*>(hr + I + c), u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = silu_mul(g[i], u[i]);
+    u32x2 o;
+    o.x = quant4(y[0], y[1], y[2], y[3], s);
+    o.y = quant4(y[4], y[5], y[6], y[7], s);
+    *reinterpret_cast<u32x2*>(qr + c) = o;
+  }
+  if (threadIdx.x == 0) scale[row] = s;
+}
+
+// One wave per token. Each lane holds experts lane, lane + 64, ... (up to
+// E = 1024); the k largest logits are picked one at a time by a wave-wide
+// (value desc, index asc) reduction. Softmax is monotonic, so these are the
+// top-k of the softmax; the weights are exp(l - l_max) normalised over the
+// chosen k (renormalize) or over all E.
+constexpr int kMaxPerLane = 16;
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+__global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int64_t ld, int M,
+                                                          int E, int k, int renormalize, int32_t* __restrict__ ids,
+                                                          float* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;   // whole wave leaves together
+  const float* lr = logits + m * ld;
+  float v[kMaxPerLane];
+#pragma unroll
+  for (int j = 0; j < kMaxPerLane; ++j) {
+    const int e = j * 64 + lane;
+    v[j] = e < E ? lr[e] : -INFINITY;
+  }
+  float top_v = 0.f;      // logit of the largest expert
+  float chosen_sum = 0.f;
+  float my_w = 0.f;       // lane j < k keeps the j-th pick
+  int my_id = 0;
+  for (int t = 0; t < k; ++t) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; ++j) {
+      const int e = j * 64 + lane;
+      if (e < E && better(v[j], e, bv, bi)) {
+        bv = v[j];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (better(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (t == 0) top_v = bv;
+    const float w = expf(bv - top_v);
+    chosen_sum += w;
+    if (lane == t) {
+      my_w = w;
+      my_id = bi;
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; ++j)
+      if (j * 64 + lane == bi) v[j] = -INFINITY;
+  }
+  float denom = chosen_sum;
+  if (!renormalize) {
+    // full softmax denominator over all E experts (the chosen ones were
+    // cleared above, so add their terms back from chosen_sum)
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; ++j)
+      if (j * 64 + lane < E && v[j] != -INFINITY) s += expf(v[j] - top_v);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    denom = chosen_sum + s;
+  }
+  if (lane < k) {
+    ids[m * k + lane] = my_id;
+    weights[m * k + lane] = my_w / denom;
+  }
+}
+
+// out[m, n] = bf16( sum_j w[m, j] * y[m * topk + j, n] ) with the products
+// and sums in fp32 in j order (w = 1 when weights is null). One thread per
+// 8 columns; N % 8 == 0.
+__global__ __launch_bounds__(256) void combine_topk_kernel(const uint16_t* __restrict__ y, int64_t ldy, int topk,
+                                                           int N, const float* __restrict__ weights,
+                                                           uint16_t* __restrict__ out, int64_t ldo) {
+  // separate float32 rounding of each product and sum (no fused multiply-add)
+#pragma clang fp contract(off)
+  const int64_t m = blockIdx.y;
+  const int c = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (c >= N) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < topk; ++j) {
+    float f[8];
+    unpack8(*reinterpret_cast<const u32x4*>(y + (m * topk + j) * ldy + c), f);
+    if (weights) {
+      const float w = weights[m * topk + j];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p = w * f[i];
+        acc[i] = acc[i] + p;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = acc[i] + f[i];
+    }
+  }
+  u32x4 o;
+  uint32_t b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) b[i] = bf16_rne_bits(__float_as_uint(acc[i]));
+  o.x = b[0] | (b[1] << 16);
+  o.y = b[2] | (b[3] << 16);
+  o.z = b[4] | (b[5] << 16);
+  o.w = b[6] | (b[7] << 16);
+  *reinterpret_cast<u32x4*>(out + m * ldo + c) = o;
+}
+
+}  // namespace
+
+hipError_t launch_quant_rows(const uint16_t* x, int64_t ldx, int M, int K, int8_t* q, int64_t ldq, float* scale,
+                             hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  hipLaunchKernelGGL(quant_rows_kernel, dim3(M), dim3(kRowThreads), 0, s, x, ldx, K, q, ldq, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int P, int I, int8_t* q, int64_t ldq,
+                                 float* scale, hipStream_t s) {
+  if (P == 0) return hipSuccess;
+  hipLaunchKernelGGL(silu_mul_quant_kernel, dim3(P), dim3(kRowThreads), 0, s, h, ldh, I, q, ldq, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_router_topk(const float* logits, int64_t ld, int M, int E, int k, int renormalize, int32_t* ids,
+                              float* weights, hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  hipLaunchKernelGGL(router_topk_kernel, dim3((M + 3) / 4), dim3(256), 0, s, logits, ld, M, E, k, renormalize,
+                     ids, weights);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine_topk(const uint16_t* y, int64_t ldy, int M, int topk, int N, const float* weights,
+                               uint16_t* out, int64_t ldo, hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  dim3 grid((N / 8 + 255) / 256, M);
+  hipLaunchKernelGGL(combine_topk_kernel, grid, dim3(256), 0, s, y, ldy, topk, N, weights, out, ldo);
+  return hipGetLastError();
+}
+
+}  // namespace mw4a8

@@ -72,4 +72,14 @@ hipError_t launch_grouped_gemm(GemmArgs a, const TileConfig& cfg, int group_size
 
 hipError_t launch_debug_partials(GemmArgs a, int group_size, int max_blocks, hipStream_t s);
 
+// MoE-layer kernels around the GEMM (moe_layer.hip); shapes checked by the caller.
+hipError_t launch_quant_rows(const uint16_t* x, int64_t ldx, int M, int K, int8_t* q, int64_t ldq, float* scale,
+                             hipStream_t s);
+hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int P, int I, int8_t* q, int64_t ldq,
+                                 float* scale, hipStream_t s);
+hipError_t launch_router_topk(const float* logits, int64_t ld, int M, int E, int k, int renormalize, int32_t* ids,
+                              float* weights, hipStream_t s);
+hipError_t launch_combine_topk(const uint16_t* y, int64_t ldy, int M, int topk, int N, const float* weights,
+                               uint16_t* out, int64_t ldo, hipStream_t s);
+
 }  // namespace mw4a8

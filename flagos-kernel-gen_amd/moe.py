@@ -187,26 +187,30 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_m: int, num_experts: int)
 
 
 def w4a8_fused_moe(x_q: torch.Tensor, x_scale: torch.Tensor, w_q4_packed: torch.Tensor, w_scale: torch.Tensor,
-                   w_zero: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
+                   w_zero: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor | None,
                    group_size: int = 128, out: torch.Tensor | None = None, block_m: int | None = None,
                    routing=None) -> torch.Tensor:
     """Routed W4A8 MoE GEMM: one bf16 row per token-expert pair.
 
     ``out[m * topk + j] = bf16((acc_e(x_q[m]) * x_scale[m]) * topk_weights[m, j])``
-    with ``e = topk_ids[m, j]``. ``routing`` may pass precomputed
+    with ``e = topk_ids[m, j]`` (``topk_weights=None``: weight 1, as for the
+    up/gate GEMM of a MoE layer). ``routing`` may pass precomputed
     ``moe_align_block_size`` results for the same ``block_m``.
     """
     M, K = x_q.shape
     _check_activations(x_q, x_scale, M)
     E, N, G = _check_weights(w_q4_packed, w_scale, w_zero, K, group_size)
     _dtype(topk_ids, "topk_ids", torch.int32)
-    _dtype(topk_weights, "topk_weights", torch.float32)
     _need(topk_ids.dim() == 2 and topk_ids.shape[0] == M, f"topk_ids must be [{M}, topk]")
     topk = topk_ids.shape[1]
-    _need(tuple(topk_weights.shape) == (M, topk) and topk_weights.is_contiguous(),
-          f"topk_weights must be a contiguous [{M}, {topk}] tensor")
-    dev = _on_gpu(dict(x_q=x_q, x_scale=x_scale, w_q4_packed=w_q4_packed, w_scale=w_scale, w_zero=w_zero,
-                       topk_ids=topk_ids, topk_weights=topk_weights))
+    tensors = dict(x_q=x_q, x_scale=x_scale, w_q4_packed=w_q4_packed, w_scale=w_scale, w_zero=w_zero,
+                   topk_ids=topk_ids)
+    if topk_weights is not None:
+        _dtype(topk_weights, "topk_weights", torch.float32)
+        _need(tuple(topk_weights.shape) == (M, topk) and topk_weights.is_contiguous(),
+              f"topk_weights must be a contiguous [{M}, {topk}] tensor")
+        tensors["topk_weights"] = topk_weights
+    dev = _on_gpu(tensors)
     P = M * topk
     if out is None:
         out = torch.empty(P, N, dtype=torch.bfloat16, device=dev)
@@ -228,7 +232,8 @@ def w4a8_fused_moe(x_q: torch.Tensor, x_scale: torch.Tensor, w_q4_packed: torch.
     sorted_ids, expert_ids, num_post = routing[0], routing[1], routing[2]
     rc = _lib.lib().mw4a8_fused_moe(_ptr(x_q), x_q.stride(0), _ptr(x_scale), _ptr(w_q4_packed), _ptr(w_scale),
                                     _ptr(w_zero), _ptr(sorted_ids), _ptr(expert_ids), _ptr(num_post),
-                                    _ptr(topk_weights), topk, _ptr(out), out.stride(0), M, N, K, E, group_size,
+                                    _ptr(topk_weights) if topk_weights is not None else None, topk, _ptr(out),
+                                    out.stride(0), M, N, K, E, group_size,
                                     block_m, ctypes.c_void_p(_stream(dev)))
     _lib.check(rc, "mw4a8_fused_moe")
     return out

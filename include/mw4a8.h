@@ -109,7 +109,8 @@ int mw4a8_moe_align(const int32_t* topk_ids, int num_pairs, int E, int block_m, 
  * counterpart; per pair i = m * topk + j routed to expert e:
  *   out[i, n] = bf16( (acc_e(x_q[m])[n] * x_scale[m]) * topk_weights[i] )
  * where acc_e is the reference reduction of docs/Task1.md:99-107.
- *  x_q [M, K] int8 (stride ldx), x_scale [M], topk_weights [M * topk] fp32,
+ *  x_q [M, K] int8 (stride ldx), x_scale [M], topk_weights [M * topk] fp32
+ *  (NULL: every weight is 1, e.g. for the up/gate GEMM of a MoE layer),
  *  sorted_ids / expert_ids / num_post_pad from mw4a8_moe_align with the
  *  same block_m, out [M * topk, N] bf16 (stride ldo). Rows of pairs that are
  *  not routed are left untouched. block_m in {16, 32, 64, 128}.
@@ -130,6 +131,60 @@ int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const 
 int mw4a8_debug_partials(const int8_t* x_q, int64_t ldx, const uint8_t* w_q4, const int8_t* w_zero,
                          const int32_t* expert_offsets, int32_t* partials, int M_total, int N, int K,
                          int E, int group_size, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * ---- MoE-layer kernels around the GEMM -------------------------------------
+ * No counterpart in the reference operator (which starts from x_q / x_scale
+ * and expert_offsets and ends at the per-row bf16 output); they produce its
+ * inputs and consume its outputs to complete a MoE layer. All four stream
+ * HBM once per row (bandwidth-bound).
+ */
+
+/*
+ * Per-token symmetric int8 quantization of bf16 activations, the producer of
+ * the GEMM's x_q / x_scale: scale[m] = max(max_k |x[m,k]|, 1e-12) / 127,
+ * x_q[m,k] = clamp(round_half_even(x[m,k] / scale[m]), -127, 127), in fp32
+ * with IEEE division (bit-identical to those float32 steps on a CPU).
+ *  x_bf16 [M, K], row stride ldx elements; K, ldx multiples of 8; 16-byte aligned
+ *  x_q    [M, K] int8, row stride ldq bytes (multiple of 8); 8-byte aligned
+ *  x_scale [M] fp32
+ */
+int mw4a8_quant_rows(const uint16_t* x_bf16, int64_t ldx, int M, int K, int8_t* x_q, int64_t ldq,
+                     float* x_scale, void* stream);
+
+/*
+ * Router top-k: for each token the topk largest logits (ties: lower expert
+ * index first), ids in descending order, and weights exp(l - l_max)
+ * normalised over the chosen topk (renormalize != 0; equal to softmax, top-k,
+ * renormalise) or over all E (renormalize == 0; plain softmax probabilities).
+ * Logits are expected finite. E <= 1024, topk <= min(E, 64).
+ *  logits [M, E] fp32, row stride ld; topk_ids [M, topk] int32;
+ *  topk_weights [M, topk] fp32
+ */
+int mw4a8_router_topk(const float* logits, int64_t ld, int M, int E, int topk, int renormalize,
+                      int32_t* topk_ids, float* topk_weights, void* stream);
+
+/*
+ * SiLU-gated product and per-row int8 requantization between the up/gate and
+ * down GEMMs: with h = [gate | up] (I columns each),
+ *   y = (gate * (1 / (1 + exp(-gate)))) * up            (fp32; reference
+ *       docs/Task3.md:103-110 forward order)
+ *   scale[p] = max(max_i |y|, 1e-12) / 127, q = clamp(rne(y / scale), -127, 127)
+ *  h_bf16 [P, 2I], row stride ldh elements (multiple of 8, >= 2I); I % 8 == 0
+ *  q [P, I] int8, row stride ldq (multiple of 8); scale [P] fp32
+ */
+int mw4a8_silu_mul_quant(const uint16_t* h_bf16, int64_t ldh, int P, int I, int8_t* q, int64_t ldq,
+                         float* scale, void* stream);
+
+/*
+ * Top-k combine: out[m, n] = bf16( sum_{j < topk} w[m,j] * y[m*topk + j, n] )
+ * with each product and sum rounded in fp32 in j order; w = 1 when
+ * topk_weights is NULL (use NULL when the down GEMM already applied them).
+ *  y_bf16 [M*topk, N], row stride ldy; out_bf16 [M, N], row stride ldo;
+ *  N, ldy, ldo multiples of 8; y and out 16-byte aligned
+ */
+int mw4a8_combine_topk(const uint16_t* y_bf16, int64_t ldy, int M, int topk, int N, const float* topk_weights,
+                       uint16_t* out_bf16, int64_t ldo, void* stream);
 
 /*
  * CPU-only self-test of the operand packing helpers the kernels use

@@ -20,6 +20,10 @@ Contents
                reference consumes its result as ``expert_offsets``.
 ``brute``      Independent int64 / float64 brute force used to pin the two
                modules above on small inputs.
+``layer_ref``  The MoE-layer steps around the GEMM that this build adds (no
+               reference counterpart): per-token int8 quantization, router
+               top-k, SiLU-gated product with requantization, top-k combine,
+               and their composition into one layer.
 
 Pinning status (how each function is checked before it is trusted) is listed
 in each module's docstring.

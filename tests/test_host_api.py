@@ -77,6 +77,43 @@ def test_c_abi_rejects_bad_arguments_without_device_work(pkg):
     assert L.mw4a8_grouped_gemm(p, 256, p, p, p, p, p, p, 64, 0, 64, 256, 2, 128, p, 1 << 20, None) == 0
 
 
+def test_layer_entries_reject_bad_arguments_without_device_work(pkg):
+    from flagos_kernel_gen_amd import _lib
+    L = _lib.lib()
+    p = ctypes.c_void_p(4096)
+    # quant: K not a multiple of 8, misaligned input, null output
+    assert L.mw4a8_quant_rows(p, 20, 4, 20, p, 24, p, None) == -1
+    assert L.mw4a8_quant_rows(ctypes.c_void_p(4098), 64, 4, 64, p, 64, p, None) == -1
+    assert L.mw4a8_quant_rows(p, 64, 4, 64, None, 64, p, None) == -1
+    assert L.mw4a8_quant_rows(p, 64, 0, 64, p, 64, p, None) == 0
+    # router: too many experts, topk > E, topk > 64
+    assert L.mw4a8_router_topk(p, 2048, 4, 2048, 8, 1, p, p, None) == -2
+    assert L.mw4a8_router_topk(p, 8, 4, 8, 9, 1, p, p, None) == -2
+    assert L.mw4a8_router_topk(p, 256, 4, 256, 65, 1, p, p, None) == -2
+    assert L.mw4a8_router_topk(p, 4, 4, 8, 2, 1, p, p, None) == -1          # ld < E
+    # silu: row stride shorter than both halves
+    assert L.mw4a8_silu_mul_quant(p, 64, 4, 64, p, 64, p, None) == -1
+    assert L.mw4a8_silu_mul_quant(p, 128, 4, 12, p, 64, p, None) == -1      # I % 8
+    # combine: N not a multiple of 8, null output, misaligned weights
+    assert L.mw4a8_combine_topk(p, 12, 4, 2, 12, None, p, 12, None) == -1
+    assert L.mw4a8_combine_topk(p, 64, 4, 2, 64, None, None, 64, None) == -1
+    assert L.mw4a8_combine_topk(p, 64, 4, 2, 64, ctypes.c_void_p(4098), p, 64, None) == -1
+
+
+def test_layer_wrappers_fail_loudly_on_cpu(pkg):
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pkg.quant_per_token(x)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pkg.router_topk(torch.zeros(4, 8), 2)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pkg.silu_mul_quant(x)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pkg.combine_topk(x, 2)
+    with pytest.raises(TypeError):
+        pkg.quant_per_token(x.float())
+
+
 def _cpu_args(M=4, E=2, N=32, K=256, gs=128):
     return (torch.zeros(M, K, dtype=torch.int8), torch.ones(M), torch.zeros(E, N, K // 2, dtype=torch.uint8),
             torch.ones(E, N, K // gs), torch.full((E, N, K // gs), 8, dtype=torch.int8),
