@@ -151,6 +151,60 @@ def measure_point(pt, steps, warmup):
     }
 
 
+LAYER_POINTS = ("dsv3_layer:64", "dsv3_layer:4096")
+
+
+class LayerPoint:
+    """One DeepSeek-V3-shape MoE layer (E=256, topk=8, hidden 7168, expert
+    intermediate 2048): bf16 tokens + router logits in, bf16 tokens out."""
+
+    E, H, I, TOPK, GS = 256, 7168, 2048, 8, 128
+
+    def __init__(self, pkg, M, dev):
+        import torch
+        wl = pkg.workloads
+        self.pkg, self.M = pkg, M
+        g = torch.Generator(device=dev).manual_seed(7000 + M)
+        self.x = torch.randn(M, self.H, generator=g, device=dev).to(torch.bfloat16)
+        self.logits = torch.randn(M, self.E, generator=g, device=dev)
+        self.w13 = wl.make_weights(self.E, 2 * self.I, self.H, self.GS, seed=7101, device=dev)
+        self.w2 = wl.make_weights(self.E, self.H, self.I, self.GS, seed=7102, device=dev)
+        _, self.mid = self.layer(return_intermediates=True)
+        torch.cuda.synchronize()
+
+    def layer(self, i=0, return_intermediates=False):
+        return self.pkg.w4a8_moe_layer(self.x, self.logits, *self.w13, *self.w2, topk=self.TOPK,
+                                       group_size=self.GS, return_intermediates=return_intermediates)
+
+    def stages(self):
+        """(name, fn, algorithmic bytes) of the streaming kernels of the layer."""
+        M, H, I, E, k = self.M, self.H, self.I, self.E, self.TOPK
+        P = M * k
+        pkg, mid = self.pkg, self.mid
+        return [
+            ("quant_rows", lambda i: pkg.quant_per_token(self.x), M * H * 2 + M * H + 4 * M),
+            ("router_topk", lambda i: pkg.router_topk(self.logits, k), M * E * 4 + M * k * 8),
+            ("silu_mul_quant", lambda i: pkg.silu_mul_quant(mid["h"]), P * 2 * I * 2 + P * I + 4 * P),
+            ("combine_topk", lambda i: pkg.combine_topk(mid["y"], k), P * H * 2 + M * H * 2),
+        ]
+
+
+def measure_layer(pkg, M, dev, steps, warmup):
+    import torch
+    lp = LayerPoint(pkg, M, dev)
+    us = time_steps(lp.layer, steps, warmup) * 1e6
+    out = {"workload": f"dsv3_layer:M={M}", "E": lp.E, "topk": lp.TOPK, "hidden": lp.H, "intermediate": lp.I,
+           "us_per_layer": round(us, 2), "stages": []}
+    for name, fn, nbytes in lp.stages():
+        t, _ = kernel_events(fn, steps, warmup)
+        out["stages"].append({"kernel": name, "us": round(t, 2), "alg_bytes": int(nbytes),
+                              "GBps": round(nbytes / (t * 1e-6) / 1e9, 1),
+                              "hbm_frac": round(nbytes / (t * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+    del lp
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(pkg, budget_s):
     """Oracle restatement of the reference operator on the host cores.
 
@@ -215,6 +269,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--headline-only", action="store_true")
+    ap.add_argument("--no-layer", action="store_true", help="skip the whole-MoE-layer measurements")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB int32 read+write kernel (torch.neg) to calibrate "
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE against known bytes")
@@ -253,6 +308,14 @@ def main():
             log(json.dumps(points[-1]))
             del pt
             torch.cuda.empty_cache()
+
+    layers = []
+    if not args.headline_only and not args.no_layer:
+        for item in LAYER_POINTS:
+            M = int(item.split(":")[1])
+            log(f"layer dsv3 M={M}")
+            layers.append(measure_layer(pkg, M, dev, max(args.steps, 20), args.warmup))
+            log(json.dumps(layers[-1]))
 
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.int32, device=dev)
@@ -294,6 +357,7 @@ def main():
         "cpu_baseline": cpu,
         "headline": head,
         "points": points,
+        "layers": layers,
     }
     print(json.dumps(line), flush=True)
 

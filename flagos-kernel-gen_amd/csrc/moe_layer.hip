@@ -70,31 +70,62 @@ __device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, f
          ((uint32_t)(qd & 0xff) << 24);
 }
 
-// One workgroup per row; K % 8 == 0, rows 16-byte aligned (checked on the host).
+// One workgroup per row; K % 8 == 0, rows 16-byte aligned (checked on the
+// host). CH > 0: the row (at most CH 8-element chunks per thread) is read
+// once and kept in registers between the max and the quantization; CH == 0
+// reads it twice (any K).
+template <int CH>
 __global__ __launch_bounds__(kRowThreads) void quant_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                  int K, int8_t* __restrict__ q, int64_t ldq,
                                                                  float* __restrict__ scale) {
   __shared__ float s_red[kRowThreads / 64];
   const int64_t row = blockIdx.x;
   const uint16_t* xr = x + row * ldx;
-  float amax = 0.f;
-  for (int c = threadIdx.x * 8; c < K; c += kRowThreads * 8) {
-    float f[8];
-    unpack8(*reinterpret_cast<const u32x4*>(xr + c), f);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
-  }
-  const float s = row_scale(block_max(amax, s_red));
   int8_t* qr = q + row * ldq;
-  for (int c = threadIdx.x * 8; c < K; c += kRowThreads * 8) {
-    float f[8];
-    unpack8(*reinterpret_cast<const u32x4*>(xr + c), f);
-    u32x2 o;
-    o.x = quant4(f[0], f[1], f[2], f[3], s);
-    o.y = quant4(f[4], f[5], f[6], f[7], s);
-    *reinterpret_cast<u32x2*>(qr + c) = o;
+  float amax = 0.f;
+  if constexpr (CH > 0) {
+    u32x4 v[CH];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = (threadIdx.x + j * kRowThreads) * 8;
+      v[j] = c < K ? *reinterpret_cast<const u32x4*>(xr + c) : u32x4{0, 0, 0, 0};
+      float f[8];
+      unpack8(v[j], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
+    }
+    const float s = row_scale(block_max(amax, s_red));
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = (threadIdx.x + j * kRowThreads) * 8;
+      if (c < K) {
+        float f[8];
+        unpack8(v[j], f);
+        u32x2 o;
+        o.x = quant4(f[0], f[1], f[2], f[3], s);
+        o.y = quant4(f[4], f[5], f[6], f[7], s);
+        *reinterpret_cast<u32x2*>(qr + c) = o;
+      }
+    }
+    if (threadIdx.x == 0) scale[row] = s;
+  } else {
+    for (int c = threadIdx.x * 8; c < K; c += kRowThreads * 8) {
+      float f[8];
+      unpack8(*reinterpret_cast<const u32x4*>(xr + c), f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
+    }
+    const float s = row_scale(block_max(amax, s_red));
+    for (int c = threadIdx.x * 8; c < K; c += kRowThreads * 8) {
+      float f[8];
+      unpack8(*reinterpret_cast<const u32x4*>(xr + c), f);
+      u32x2 o;
+      o.x = quant4(f[0], f[1], f[2], f[3], s);
+      o.y = quant4(f[4], f[5], f[6], f[7], s);
+      *reinterpret_cast<u32x2*>(qr + c) = o;
+    }
+    if (threadIdx.x == 0) scale[row] = s;
   }
-  if (threadIdx.x == 0) scale[row] = s;
 }
 
 // y = silu(gate) * up in fp32 as sigmoid = 1 / (1 + exp(-g)), silu = g *
@@ -104,7 +135,9 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return (g * sg) * u;
 }
 
-// One workgroup per row of h = [gate (I) | up (I)] bf16; I % 8 == 0.
+// One workgroup per row of h = [gate (I) | up (I)] bf16; I % 8 == 0. CH as
+// in quant_rows_kernel (the products y are kept in registers).
+template <int CH>
 __global__ __launch_bounds__(kRowThreads) void silu_mul_quant_kernel(const uint16_t* __restrict__ h,
                                                                      int64_t ldh, int I, int8_t* __restrict__ q,
                                                                      int64_t ldq, float* __restrict__ scale) {
@@ -112,6 +145,38 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_quant_kernel(const uint1
   const int64_t row = blockIdx.x;
   const uint16_t* hr = h + row * ldh;
   float amax = 0.f;
+  if constexpr (CH > 0) {
+    float y[CH][8];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = (threadIdx.x + j * kRowThreads) * 8;
+      const bool ok = c < I;
+      const u32x4 gv = ok ? *reinterpret_cast<const u32x4*>(hr + c) : u32x4{0, 0, 0, 0};
+      const u32x4 uv = ok ? *reinterpret_cast<const u32x4*>(hr + I + c) : u32x4{0, 0, 0, 0};
+      float g[8], u[8];
+      unpack8(gv, g);
+      unpack8(uv, u);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        y[j][i] = silu_mul(g[i], u[i]);
+        amax = fmaxf(amax, fabsf(y[j][i]));
+      }
+    }
+    const float s = row_scale(block_max(amax, s_red));
+    int8_t* qr = q + row * ldq;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = (threadIdx.x + j * kRowThreads) * 8;
+      if (c < I) {
+        u32x2 o;
+        o.x = quant4(y[j][0], y[j][1], y[j][2], y[j][3], s);
+        o.y = quant4(y[j][4], y[j][5], y[j][6], y[j][7], s);
+        *reinterpret_cast<u32x2*>(qr + c) = o;
+      }
+    }
+    if (threadIdx.x == 0) scale[row] = s;
+    return;
+  }
   for (int c = threadIdx.x * 8; c < I; c += kRowThreads * 8) {
     float g[8], u[8];
     unpack8(*reinterpret_cast<const u32x4*>(hr + c), g);
@@ -250,17 +315,31 @@ __global__ __launch_bounds__(256) void combine_topk_kernel(const uint16_t* __res
 
 }  // namespace
 
+// chunks of 8 elements per thread needed to hold a row of n elements
+static int row_chunks(int n) { return (n + kRowThreads * 8 - 1) / (kRowThreads * 8); }
+
 hipError_t launch_quant_rows(const uint16_t* x, int64_t ldx, int M, int K, int8_t* q, int64_t ldq, float* scale,
                              hipStream_t s) {
   if (M == 0) return hipSuccess;
-  hipLaunchKernelGGL(quant_rows_kernel, dim3(M), dim3(kRowThreads), 0, s, x, ldx, K, q, ldq, scale);
+  const int ch = row_chunks(K);
+  const dim3 g(M), b(kRowThreads);
+  if (ch <= 1) hipLaunchKernelGGL(quant_rows_kernel<1>, g, b, 0, s, x, ldx, K, q, ldq, scale);
+  else if (ch <= 2) hipLaunchKernelGGL(quant_rows_kernel<2>, g, b, 0, s, x, ldx, K, q, ldq, scale);
+  else if (ch <= 4) hipLaunchKernelGGL(quant_rows_kernel<4>, g, b, 0, s, x, ldx, K, q, ldq, scale);
+  else if (ch <= 8) hipLaunchKernelGGL(quant_rows_kernel<8>, g, b, 0, s, x, ldx, K, q, ldq, scale);
+  else hipLaunchKernelGGL(quant_rows_kernel<0>, g, b, 0, s, x, ldx, K, q, ldq, scale);
   return hipGetLastError();
 }
 
 hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int P, int I, int8_t* q, int64_t ldq,
                                  float* scale, hipStream_t s) {
   if (P == 0) return hipSuccess;
-  hipLaunchKernelGGL(silu_mul_quant_kernel, dim3(P), dim3(kRowThreads), 0, s, h, ldh, I, q, ldq, scale);
+  const int ch = row_chunks(I);
+  const dim3 g(P), b(kRowThreads);
+  if (ch <= 1) hipLaunchKernelGGL(silu_mul_quant_kernel<1>, g, b, 0, s, h, ldh, I, q, ldq, scale);
+  else if (ch <= 2) hipLaunchKernelGGL(silu_mul_quant_kernel<2>, g, b, 0, s, h, ldh, I, q, ldq, scale);
+  else if (ch <= 4) hipLaunchKernelGGL(silu_mul_quant_kernel<4>, g, b, 0, s, h, ldh, I, q, ldq, scale);
+  else hipLaunchKernelGGL(silu_mul_quant_kernel<0>, g, b, 0, s, h, ldh, I, q, ldq, scale);
   return hipGetLastError();
 }
 

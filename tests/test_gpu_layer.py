@@ -31,7 +31,8 @@ def _close(got, ref, what, rel=2e-2, cos_min=0.9995):
 
 # ---------------------------------------------------------------- quant
 
-@pytest.mark.parametrize("M,K", [(1, 8), (5, 1024), (64, 7168), (4096, 2048), (3, 40000)])
+@pytest.mark.parametrize("M,K", [(1, 8), (5, 1024), (64, 7168), (4096, 2048), (7, 3000), (9, 16384),
+                                 (3, 40000)])
 def test_quant_rows_bit_exact(pkg, dev, M, K):
     print(f"[quant] M={M} K={K}", flush=True)
     g = torch.Generator().manual_seed(M + K)
@@ -87,7 +88,8 @@ def test_router_matches_the_benchmark_routing(pkg, dev):
 
 # ---------------------------------------------------------------- silu * up
 
-@pytest.mark.parametrize("P,I", [(1, 8), (37, 768), (512, 2048), (4096, 1024)])
+@pytest.mark.parametrize("P,I", [(1, 8), (37, 768), (512, 2048), (4096, 1024), (9, 3000), (7, 6144),
+                                 (5, 10000)])
 def test_silu_mul_quant(pkg, dev, P, I):
     print(f"[silu] P={P} I={I}", flush=True)
     g = torch.Generator().manual_seed(P + I)
