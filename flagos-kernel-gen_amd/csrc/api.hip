@@ -116,7 +116,7 @@ int run_csr(GemmArgs a, const int32_t* offsets, int M_total, int E, int gs, void
   a.blk_row0 = w.row0;
   a.blk_row1 = w.row1;
   a.blk_count = w.count;
-  e = debug ? launch_debug_partials(a, gs, max_blocks, s) : launch_grouped_gemm(a, cfg, gs, false, max_blocks, s);
+  e = debug ? launch_debug_partials(a, gs, max_blocks, s) : launch_grouped_gemm(a, cfg, gs, kModeCsr, max_blocks, s);
   if (e != hipSuccess) return hip_fail(e, "grouped GEMM launch");
   return MW4A8_OK;
 }
@@ -199,11 +199,14 @@ int mw4a8_moe_align(const int32_t* topk_ids, int num_pairs, int E, int block_m, 
   return MW4A8_OK;
 }
 
-int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
-                    const float* w_scale, const int8_t* w_zero, const int32_t* sorted_ids,
-                    const int32_t* expert_ids, const int32_t* num_post_pad, const float* topk_weights,
-                    int topk, uint16_t* out_bf16, int64_t ldo, int M, int N, int K, int E, int group_size,
-                    int block_m, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int fused_moe_impl(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4, const float* w_scale,
+                   const int8_t* w_zero, const int32_t* sorted_ids, const int32_t* expert_ids,
+                   const int32_t* num_post_pad, const float* topk_weights, int topk, uint16_t* out_bf16, int64_t ldo,
+                   int M, int N, int K, int E, int group_size, int block_m, int mode, void* stream) {
   g_err[0] = 0;
   if (topk <= 0) return fail(MW4A8_ERR_INVALID, "topk=%d", topk);
   if (M == 0) return MW4A8_OK;
@@ -233,8 +236,46 @@ int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const 
   const TileConfig cfg = tiles_for_block_m(block_m, group_size);
   if (cfg.BM != block_m) return fail(MW4A8_ERR_UNSUPPORTED, "block_m must be 16, 32, 64 or 128");
   const int max_blocks = max_row_blocks((int)pairs, E, block_m);
-  hipError_t e = launch_grouped_gemm(a, cfg, group_size, true, max_blocks, static_cast<hipStream_t>(stream));
+  hipError_t e = launch_grouped_gemm(a, cfg, group_size, mode, max_blocks, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "fused MoE launch");
+  return MW4A8_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
+                    const float* w_scale, const int8_t* w_zero, const int32_t* sorted_ids,
+                    const int32_t* expert_ids, const int32_t* num_post_pad, const float* topk_weights,
+                    int topk, uint16_t* out_bf16, int64_t ldo, int M, int N, int K, int E, int group_size,
+                    int block_m, void* stream) {
+  return fused_moe_impl(x_q, ldx, x_scale, w_q4, w_scale, w_zero, sorted_ids, expert_ids, num_post_pad,
+                        topk_weights, topk, out_bf16, ldo, M, N, K, E, group_size, block_m, kModeRouted, stream);
+}
+
+int mw4a8_fused_moe_repacked(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_mfma,
+                             const float* w_scale, const int8_t* w_zero, const int32_t* sorted_ids,
+                             const int32_t* expert_ids, const int32_t* num_post_pad, const float* topk_weights,
+                             int topk, uint16_t* out_bf16, int64_t ldo, int M, int N, int K, int E,
+                             int group_size, int block_m, void* stream) {
+  return fused_moe_impl(x_q, ldx, x_scale, w_mfma, w_scale, w_zero, sorted_ids, expert_ids, num_post_pad,
+                        topk_weights, topk, out_bf16, ldo, M, N, K, E, group_size, block_m, kModeRoutedRepacked,
+                        stream);
+}
+
+int mw4a8_repack_weights(const uint8_t* src, uint8_t* dst, int64_t E, int N, int K, int inverse, void* stream) {
+  g_err[0] = 0;
+  if (E < 0 || N < 0 || K <= 0 || K % 8 != 0)
+    return fail(MW4A8_ERR_INVALID, "bad sizes: E=%lld N=%d K=%d (K must be a multiple of 8)", (long long)E, N, K);
+  const int64_t bytes = E * (int64_t)N * (K / 2);
+  if (bytes == 0) return MW4A8_OK;
+  if (!src || !dst) return fail(MW4A8_ERR_INVALID, "null tensor pointer");
+  if (!aligned(src, 16) || !aligned(dst, 16)) return fail(MW4A8_ERR_INVALID, "weights must be 16-byte aligned");
+  if (src == dst) return fail(MW4A8_ERR_INVALID, "in-place repack is not supported");
+  hipError_t e = launch_repack_weights(reinterpret_cast<const uint32_t*>(src), reinterpret_cast<uint32_t*>(dst),
+                                       bytes / 4, inverse ? 1 : 0, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "repack launch");
   return MW4A8_OK;
 }
 

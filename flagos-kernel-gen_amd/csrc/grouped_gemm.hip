@@ -169,7 +169,7 @@ struct TileCtx {
 //     zero-point / scale runs are aligned; the loop then carries no guards.
 //     (Used for the 16- and 32-row tiles only: without the guards the
 //     compiler schedules the larger bodies into scratch.)
-template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, bool ROUTED, bool DEBUGP, bool FAST>
+template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, int8_t* s_x, float* s_scale,
                                           int8_t* s_zero, const int* s_src, const int* s_dst, const float* s_xs,
                                           const float* s_tw) {
@@ -185,6 +185,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   constexpr int UPR = KC / 16;        // 16-byte units per row and chunk
   constexpr int XU = (BMX * UPR + NT - 1) / NT;
   constexpr bool ZS_LDS = ZSG > 0;
+  constexpr bool ROUTED = RMODE != 0;
+  constexpr bool REPACKED = RMODE == kModeRoutedRepacked;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -265,12 +267,17 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 #pragma unroll
     for (int j = 0; j < XU; ++j) {
       const u32x4 v = xr[j];
-      u32x4 p;
-      p.x = even_bytes(v.x, v.y);
-      p.y = odd_bytes(v.x, v.y);
-      p.z = even_bytes(v.z, v.w);
-      p.w = odd_bytes(v.z, v.w);
-      *reinterpret_cast<u32x4*>(s_x + buf * BUF + x_lds[j]) = p;
+      if constexpr (REPACKED) {
+        // the repacked weights unpack in natural K order: no relabel
+        *reinterpret_cast<u32x4*>(s_x + buf * BUF + x_lds[j]) = v;
+      } else {
+        u32x4 p;
+        p.x = even_bytes(v.x, v.y);
+        p.y = odd_bytes(v.x, v.y);
+        p.z = even_bytes(v.z, v.w);
+        p.w = odd_bytes(v.z, v.w);
+        *reinterpret_cast<u32x4*>(s_x + buf * BUF + x_lds[j]) = p;
+      }
     }
   };
 
@@ -365,8 +372,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
             sv[nb] *= 0.0625f;
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-              const uint32_t t0 = wc.w[g][nb][2 * s] ^ 0x88888888u;
-              const uint32_t t1 = wc.w[g][nb][2 * s + 1] ^ 0x88888888u;
+              // repacked weights store every nibble with its top bit flipped
+              const uint32_t t0 = REPACKED ? wc.w[g][nb][2 * s] : wc.w[g][nb][2 * s] ^ 0x88888888u;
+              const uint32_t t1 = REPACKED ? wc.w[g][nb][2 * s + 1] : wc.w[g][nb][2 * s + 1] ^ 0x88888888u;
               bfr[nb][s].x = (int)((t0 << 4) & 0xF0F0F0F0u);
               bfr[nb][s].y = (int)(t0 & 0xF0F0F0F0u);
               bfr[nb][s].z = (int)((t1 << 4) & 0xF0F0F0F0u);
@@ -379,8 +387,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
             const ZeroFold zf = make_zero_fold(zv[nb]);
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-              const uint32_t d0 = wc.w[g][nb][2 * s];
-              const uint32_t d1 = wc.w[g][nb][2 * s + 1];
+              const uint32_t flip = REPACKED ? 0x88888888u : 0u;
+              const uint32_t d0 = wc.w[g][nb][2 * s] ^ flip;
+              const uint32_t d1 = wc.w[g][nb][2 * s + 1] ^ flip;
               bfr[nb][s].x = (int)fold_even(d0, zf);
               bfr[nb][s].y = (int)fold_odd(d0, zf);
               bfr[nb][s].z = (int)fold_even(d1, zf);
@@ -492,13 +501,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 
 // ZSG > 0: zero points and scales come from an LDS copy of the tile's
 // block; the host launches this only when G <= ZSG (see zs_block_fits).
-template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, bool ROUTED, bool DEBUGP, bool FAST,
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST,
           int WAVES_PER_EU>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU)))
 void w4a8_gemm_kernel(const GemmArgs a) {
   constexpr int BN = NW * WN;
   constexpr int PITCH = KCG * GS + 32;
   constexpr bool ZS_LDS = ZSG > 0;
+  constexpr bool ROUTED = RMODE != 0;
   static_assert(BM % 16 == 0 && WN % 16 == 0 && GS % 64 == 0, "tile shape");
 
   __shared__ __attribute__((aligned(16))) int8_t s_x[2 * BM * PITCH];
@@ -583,12 +593,12 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   // tiles whose valid rows fit in the top half run the half-height body
   if constexpr (BM >= 64) {
     if (rows <= BM / 2) {
-      gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP, FAST>(a, c, s_x, s_scale, s_zero, s_src, s_dst,
+      gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST>(a, c, s_x, s_scale, s_zero, s_src, s_dst,
                                                                      s_xs, s_tw);
       return;
     }
   }
-  gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP, FAST>(a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs, s_tw);
+  gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST>(a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs, s_tw);
 }
 
 // ---------------------------------------------------------------------------
@@ -609,7 +619,7 @@ static bool zs_block_fits(const GemmArgs& a, int BN, int ZSG) {
          reinterpret_cast<uintptr_t>(a.wz) % 16 == 0 && (a.ws == nullptr || reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
 }
 
-template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, bool ROUTED, bool DEBUGP, int WPE>
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, int WPE>
 static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   set_grid(a, max_blocks, NW * WN, R);
   // a column's KCG zero points / scales of one chunk can be read as one
@@ -621,15 +631,15 @@ static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   // unroll, and (without the LDS zero/scale block) aligned vector runs
   constexpr bool CAN_FAST = !DEBUGP && BM <= 32;
   if (CAN_FAST && a.G % (KCG * RD) == 0 && (ZSG > 0 || a.zs_vec))
-    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP, CAN_FAST, WPE>),
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, CAN_FAST, WPE>),
                        dim3(8 * a.per_xcd), dim3(NW * 64), 0, s, a);
   else
-    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, ROUTED, DEBUGP, false, WPE>),
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, WPE>),
                        dim3(8 * a.per_xcd), dim3(NW * 64), 0, s, a);
   return hipGetLastError();
 }
 
-template <int GS, bool ROUTED>
+template <int GS, int RMODE>
 static hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, hipStream_t s) {
   constexpr int K512 = 512 / GS > 0 ? 512 / GS : 1;     // groups per 512 bytes of K
   constexpr int K1024 = 1024 / GS > 0 ? 1024 / GS : 1;
@@ -639,35 +649,42 @@ static hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, h
       if (zs_block_fits(a, 64, 64)) {
         // few tiles (decode of a handful of tokens): deeper chunks per wave
         if ((int64_t)max_blocks * ((a.N + 63) / 64) < 1024)
-          return launch_one<16, 16, 4, GS, K1024, 2, 64, ROUTED, false, 1>(a, max_blocks, c.R, s);
-        return launch_one<16, 16, 4, GS, K512, 2, 64, ROUTED, false, 1>(a, max_blocks, c.R, s);
+          return launch_one<16, 16, 4, GS, K1024, 2, 64, RMODE, false, 1>(a, max_blocks, c.R, s);
+        return launch_one<16, 16, 4, GS, K512, 2, 64, RMODE, false, 1>(a, max_blocks, c.R, s);
       }
-      return launch_one<16, 16, 4, GS, K1024, 2, 0, ROUTED, false, 1>(a, max_blocks, c.R, s);
+      return launch_one<16, 16, 4, GS, K1024, 2, 0, RMODE, false, 1>(a, max_blocks, c.R, s);
     case 32:
-      if (zs_block_fits(a, 64, 64)) return launch_one<32, 16, 4, GS, K512, 2, 64, ROUTED, false, 1>(a, max_blocks, c.R, s);
-      return launch_one<32, 16, 4, GS, K512, 2, 0, ROUTED, false, 1>(a, max_blocks, c.R, s);
+      if (zs_block_fits(a, 64, 64)) return launch_one<32, 16, 4, GS, K512, 2, 64, RMODE, false, 1>(a, max_blocks, c.R, s);
+      return launch_one<32, 16, 4, GS, K512, 2, 0, RMODE, false, 1>(a, max_blocks, c.R, s);
     // three waves per SIMD fit the gs = 128 body without spills; the others keep two
-    case 64: return launch_one<64, 32, 4, GS, K256, 2, 0, ROUTED, false, GS == 128 ? 3 : 2>(a, max_blocks, c.R, s);
-    case 128: return launch_one<128, 32, 4, GS, K256, 2, 0, ROUTED, false, 2>(a, max_blocks, c.R, s);
+    case 64: return launch_one<64, 32, 4, GS, K256, 2, 0, RMODE, false, GS == 128 ? 3 : 2>(a, max_blocks, c.R, s);
+    case 128: return launch_one<128, 32, 4, GS, K256, 2, 0, RMODE, false, 2>(a, max_blocks, c.R, s);
     default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t launch_grouped_gemm(GemmArgs a, const TileConfig& cfg, int group_size, bool routed,
-                               int max_blocks, hipStream_t s) {
-  if (group_size == 128)
-    return routed ? dispatch_bm<128, true>(a, cfg, max_blocks, s) : dispatch_bm<128, false>(a, cfg, max_blocks, s);
-  if (group_size == 64)
-    return routed ? dispatch_bm<64, true>(a, cfg, max_blocks, s) : dispatch_bm<64, false>(a, cfg, max_blocks, s);
-  if (group_size == 256)
-    return routed ? dispatch_bm<256, true>(a, cfg, max_blocks, s) : dispatch_bm<256, false>(a, cfg, max_blocks, s);
+template <int GS>
+static hipError_t dispatch_mode(GemmArgs a, const TileConfig& cfg, int mode, int max_blocks, hipStream_t s) {
+  switch (mode) {
+    case kModeCsr: return dispatch_bm<GS, kModeCsr>(a, cfg, max_blocks, s);
+    case kModeRouted: return dispatch_bm<GS, kModeRouted>(a, cfg, max_blocks, s);
+    case kModeRoutedRepacked: return dispatch_bm<GS, kModeRoutedRepacked>(a, cfg, max_blocks, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_grouped_gemm(GemmArgs a, const TileConfig& cfg, int group_size, int mode, int max_blocks,
+                               hipStream_t s) {
+  if (group_size == 128) return dispatch_mode<128>(a, cfg, mode, max_blocks, s);
+  if (group_size == 64) return dispatch_mode<64>(a, cfg, mode, max_blocks, s);
+  if (group_size == 256) return dispatch_mode<256>(a, cfg, mode, max_blocks, s);
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_debug_partials(GemmArgs a, int group_size, int max_blocks, hipStream_t s) {
-  if (group_size == 128) return launch_one<16, 16, 4, 128, 4, 2, 0, false, true, 1>(a, max_blocks, 1, s);
-  if (group_size == 64) return launch_one<16, 16, 4, 64, 8, 2, 0, false, true, 1>(a, max_blocks, 1, s);
-  if (group_size == 256) return launch_one<16, 16, 4, 256, 2, 2, 0, false, true, 1>(a, max_blocks, 1, s);
+  if (group_size == 128) return launch_one<16, 16, 4, 128, 4, 2, 0, kModeCsr, true, 1>(a, max_blocks, 1, s);
+  if (group_size == 64) return launch_one<16, 16, 4, 64, 8, 2, 0, kModeCsr, true, 1>(a, max_blocks, 1, s);
+  if (group_size == 256) return launch_one<16, 16, 4, 256, 2, 2, 0, kModeCsr, true, 1>(a, max_blocks, 1, s);
   return hipErrorInvalidValue;
 }
 

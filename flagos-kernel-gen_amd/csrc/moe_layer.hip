@@ -313,7 +313,71 @@ __global__ __launch_bounds__(256) void combine_topk_kernel(const uint16_t* __res
   *reinterpret_cast<u32x4*>(out + m * ldo + c) = o;
 }
 
+// ---- weight repack ----------------------------------------------------------
+// Reference packing: byte j of an 8-element K run holds k = 2j (low nibble)
+// and 2j + 1 (high nibble), i.e. nibble k of the run's 32-bit word is
+// element k. MFMA order: byte i holds element i (low) and i + 4 (high), each
+// nibble XORed with 8. The GEMM's even/odd nibble split then yields elements
+// 0-3 and 4-7 in natural order (no activation relabel), and 16*(u - 8) is
+// the flipped nibble shifted into the byte's high half.
+
+// 4 nibbles in bits 0-15 -> one per byte (bits 8i .. 8i+3)
+__device__ __forceinline__ uint32_t spread4(uint32_t x) {
+  x = (x | (x << 8)) & 0x00FF00FFu;
+  return (x | (x << 4)) & 0x0F0F0F0Fu;
+}
+
+// inverse of spread4
+__device__ __forceinline__ uint32_t compact4(uint32_t x) {
+  x = (x | (x >> 4)) & 0x00FF00FFu;
+  return (x | (x >> 8)) & 0x0000FFFFu;
+}
+
+__device__ __forceinline__ uint32_t to_mfma_order(uint32_t w) {
+  return (spread4(w & 0xFFFFu) | (spread4(w >> 16) << 4)) ^ 0x88888888u;
+}
+
+__device__ __forceinline__ uint32_t to_reference_order(uint32_t v) {
+  v ^= 0x88888888u;
+  return compact4(v & 0x0F0F0F0Fu) | (compact4((v >> 4) & 0x0F0F0F0Fu) << 16);
+}
+
+// grid-stride over 16-byte vectors (16-byte aligned buffers), then the
+// n_words % 4 tail words
+__global__ __launch_bounds__(256) void repack_weights_kernel(const uint32_t* __restrict__ src,
+                                                             uint32_t* __restrict__ dst, int64_t n_words,
+                                                             int inverse) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t n_vec = n_words / 4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n_vec; i += stride) {
+    u32x4 v = reinterpret_cast<const u32x4*>(src)[i];
+    if (inverse) {
+      v.x = to_reference_order(v.x);
+      v.y = to_reference_order(v.y);
+      v.z = to_reference_order(v.z);
+      v.w = to_reference_order(v.w);
+    } else {
+      v.x = to_mfma_order(v.x);
+      v.y = to_mfma_order(v.y);
+      v.z = to_mfma_order(v.z);
+      v.w = to_mfma_order(v.w);
+    }
+    reinterpret_cast<u32x4*>(dst)[i] = v;
+  }
+  const int64_t t = n_vec * 4 + (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t < n_words) dst[t] = inverse ? to_reference_order(src[t]) : to_mfma_order(src[t]);
+}
+
 }  // namespace
+
+hipError_t launch_repack_weights(const uint32_t* src, uint32_t* dst, int64_t n_words, int inverse, hipStream_t s) {
+  if (n_words == 0) return hipSuccess;
+  int64_t blocks = (n_words / 4 + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(repack_weights_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, dst, n_words, inverse);
+  return hipGetLastError();
+}
 
 // chunks of 8 elements per thread needed to hold a row of n elements
 static int row_chunks(int n) { return (n + kRowThreads * 8 - 1) / (kRowThreads * 8); }

@@ -67,8 +67,13 @@ hipError_t launch_moe_align(const int32_t* topk_ids, int num_pairs, int E, int B
                             int32_t* num_post_pad, int32_t* expert_offsets, hipStream_t s);
 
 // max_blocks bounds the row-block index space the grid covers.
-hipError_t launch_grouped_gemm(GemmArgs a, const TileConfig& cfg, int group_size, bool routed,
-                               int max_blocks, hipStream_t s);
+// Row sources and weight layout of a GEMM launch.
+constexpr int kModeCsr = 0;             // reference layout: CSR expert offsets, reference weight format
+constexpr int kModeRouted = 1;          // routed pairs (sorted_ids), reference weight format
+constexpr int kModeRoutedRepacked = 2;  // routed pairs, weights in the repacked MFMA order
+
+hipError_t launch_grouped_gemm(GemmArgs a, const TileConfig& cfg, int group_size, int mode, int max_blocks,
+                               hipStream_t s);
 
 hipError_t launch_debug_partials(GemmArgs a, int group_size, int max_blocks, hipStream_t s);
 
@@ -81,5 +86,8 @@ hipError_t launch_router_topk(const float* logits, int64_t ld, int M, int E, int
                               float* weights, hipStream_t s);
 hipError_t launch_combine_topk(const uint16_t* y, int64_t ldy, int M, int topk, int N, const float* weights,
                                uint16_t* out, int64_t ldo, hipStream_t s);
+// Weight repack between the reference int4 packing and the MFMA order
+// (inverse != 0: back to the reference packing); n_words 32-bit words.
+hipError_t launch_repack_weights(const uint32_t* src, uint32_t* dst, int64_t n_words, int inverse, hipStream_t s);
 
 }  // namespace mw4a8

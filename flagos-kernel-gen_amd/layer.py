@@ -116,13 +116,15 @@ def combine_topk(y: torch.Tensor, topk: int, topk_weights: torch.Tensor | None =
 
 def w4a8_moe_layer(x: torch.Tensor, router_logits: torch.Tensor, w13_q4: torch.Tensor, w13_scale: torch.Tensor,
                    w13_zero: torch.Tensor, w2_q4: torch.Tensor, w2_scale: torch.Tensor, w2_zero: torch.Tensor,
-                   topk: int, group_size: int = 128, renormalize: bool = True, return_intermediates: bool = False):
+                   topk: int, group_size: int = 128, renormalize: bool = True, return_intermediates: bool = False,
+                   weight_layout: str = "reference"):
     """One W4A8 MoE layer: ``x [M, H]`` bf16 -> ``out [M, H]`` bf16.
 
     ``w13_*`` hold the up/gate projection ``[E, 2I, H/2]`` (rows ``[0, I)``
     gate, ``[I, 2I)`` up), ``w2_*`` the down projection ``[E, H, I/2]``, both
     in the reference's packed int4 / group-scale / zero-point format
-    (docs/Task1.md:8-26). Steps (each a HIP kernel):
+    (docs/Task1.md:8-26), or both converted by ``repack_weights`` with
+    ``weight_layout="mfma"``. Steps (each a HIP kernel):
 
     1. ``x_q, x_scale = quant_per_token(x)``
     2. ``ids, w = router_topk(router_logits, topk, renormalize)``
@@ -144,7 +146,7 @@ def w4a8_moe_layer(x: torch.Tensor, router_logits: torch.Tensor, w13_q4: torch.T
     bm_up = select_block_m(P, E, two_i, H, group_size)
     routing_up = moe_align_block_size(ids, bm_up, E)
     h = w4a8_fused_moe(x_q, x_scale, w13_q4, w13_scale, w13_zero, ids, None, group_size=group_size,
-                       block_m=bm_up, routing=routing_up)
+                       block_m=bm_up, routing=routing_up, weight_layout=weight_layout)
     h_q, h_scale = silu_mul_quant(h)
     # the down GEMM treats every pair as a token routed to one expert: the
     # pair order and expert of row p are those of the up/gate GEMM
@@ -152,7 +154,7 @@ def w4a8_moe_layer(x: torch.Tensor, router_logits: torch.Tensor, w13_q4: torch.T
     bm_down = select_block_m(P, E, H, I, group_size)
     routing_down = routing_up if bm_down == bm_up else moe_align_block_size(ids_p, bm_down, E)
     y = w4a8_fused_moe(h_q, h_scale, w2_q4, w2_scale, w2_zero, ids_p, w.view(P, 1), group_size=group_size,
-                       block_m=bm_down, routing=routing_down)
+                       block_m=bm_down, routing=routing_down, weight_layout=weight_layout)
     out = combine_topk(y, topk)
     if return_intermediates:
         return out, dict(x_q=x_q, x_scale=x_scale, topk_ids=ids, topk_weights=w, h=h, h_q=h_q, h_scale=h_scale,

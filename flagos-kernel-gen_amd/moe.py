@@ -189,14 +189,17 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_m: int, num_experts: int)
 def w4a8_fused_moe(x_q: torch.Tensor, x_scale: torch.Tensor, w_q4_packed: torch.Tensor, w_scale: torch.Tensor,
                    w_zero: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor | None,
                    group_size: int = 128, out: torch.Tensor | None = None, block_m: int | None = None,
-                   routing=None) -> torch.Tensor:
+                   routing=None, weight_layout: str = "reference") -> torch.Tensor:
     """Routed W4A8 MoE GEMM: one bf16 row per token-expert pair.
 
     ``out[m * topk + j] = bf16((acc_e(x_q[m]) * x_scale[m]) * topk_weights[m, j])``
     with ``e = topk_ids[m, j]`` (``topk_weights=None``: weight 1, as for the
     up/gate GEMM of a MoE layer). ``routing`` may pass precomputed
     ``moe_align_block_size`` results for the same ``block_m``.
+    ``weight_layout="mfma"`` takes weights converted by ``repack_weights``
+    (bit-identical results).
     """
+    _need(weight_layout in ("reference", "mfma"), f"unknown weight_layout {weight_layout!r}")
     M, K = x_q.shape
     _check_activations(x_q, x_scale, M)
     E, N, G = _check_weights(w_q4_packed, w_scale, w_zero, K, group_size)
@@ -230,10 +233,27 @@ def w4a8_fused_moe(x_q: torch.Tensor, x_scale: torch.Tensor, w_q4_packed: torch.
               f"routing buffers do not match block_m={block_m} (expected lengths {sl} and {bl})")
         _on_gpu(dict(sorted_ids=routing[0], expert_ids=routing[1], num_tokens_post_padded=routing[2]))
     sorted_ids, expert_ids, num_post = routing[0], routing[1], routing[2]
-    rc = _lib.lib().mw4a8_fused_moe(_ptr(x_q), x_q.stride(0), _ptr(x_scale), _ptr(w_q4_packed), _ptr(w_scale),
+    entry = _lib.lib().mw4a8_fused_moe if weight_layout == "reference" else _lib.lib().mw4a8_fused_moe_repacked
+    rc = entry(_ptr(x_q), x_q.stride(0), _ptr(x_scale), _ptr(w_q4_packed), _ptr(w_scale),
                                     _ptr(w_zero), _ptr(sorted_ids), _ptr(expert_ids), _ptr(num_post),
                                     _ptr(topk_weights) if topk_weights is not None else None, topk, _ptr(out),
                                     out.stride(0), M, N, K, E, group_size,
                                     block_m, ctypes.c_void_p(_stream(dev)))
     _lib.check(rc, "mw4a8_fused_moe")
+    return out
+
+
+def repack_weights(w_q4_packed: torch.Tensor, inverse: bool = False) -> torch.Tensor:
+    """Convert ``[E, N, K/2]`` uint8 int4 weights between the reference packing
+    (docs/Task1.md:78-81) and the MFMA order ``w4a8_fused_moe(...,
+    weight_layout="mfma")`` reads (``inverse=True``: back). Returns a new
+    tensor; the round trip is bit-exact."""
+    _dtype(w_q4_packed, "w_q4_packed", torch.uint8)
+    _need(w_q4_packed.dim() == 3 and w_q4_packed.is_contiguous(), "w_q4_packed must be a contiguous [E, N, K/2]")
+    E, N, K_half = w_q4_packed.shape
+    dev = _on_gpu(dict(w_q4_packed=w_q4_packed))
+    out = torch.empty_like(w_q4_packed)
+    rc = _lib.lib().mw4a8_repack_weights(_ptr(w_q4_packed), _ptr(out), E, N, 2 * K_half, 1 if inverse else 0,
+                                         ctypes.c_void_p(_stream(dev)))
+    _lib.check(rc, "mw4a8_repack_weights")
     return out

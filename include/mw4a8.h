@@ -122,6 +122,29 @@ int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const 
                     int block_m, void* stream);
 
 /*
+ * Offline weight repack (no reference counterpart; the reference format stays
+ * the drop-in default). Within every 8-element K run of a column the
+ * reference packing (docs/Task1.md:78-81: byte j = elements 2j | 2j+1 << 4)
+ * becomes byte i = (u[i] ^ 8) | (u[i+4] ^ 8) << 4, so the GEMM unpacks its
+ * MFMA operand in natural K order (activations need no relabel) and the
+ * symmetric-zero path skips one op per word. Same size [E, N, K/2]; K % 8 ==
+ * 0; 16-byte aligned; not in place. inverse != 0 converts back (bit-exact
+ * round trip).
+ */
+int mw4a8_repack_weights(const uint8_t* src, uint8_t* dst, int64_t E, int N, int K, int inverse, void* stream);
+
+/*
+ * mw4a8_fused_moe on weights repacked by mw4a8_repack_weights (same
+ * arguments; scales and zero points unchanged). Results are bit-identical to
+ * mw4a8_fused_moe on the reference-format weights.
+ */
+int mw4a8_fused_moe_repacked(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_mfma,
+                             const float* w_scale, const int8_t* w_zero, const int32_t* sorted_ids,
+                             const int32_t* expert_ids, const int32_t* num_post_pad, const float* topk_weights,
+                             int topk, uint16_t* out_bf16, int64_t ldo, int M, int N, int K, int E,
+                             int group_size, int block_m, void* stream);
+
+/*
  * Debug export of the exact int32 per-group partial sums
  *   partials[m, n, g] = sum_{k in g} x_q[m,k] * int8(nib - zero)
  * (reference docs/Task1.md:99-104, the "mgk,ngk->mng" einsum) for the

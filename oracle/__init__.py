@@ -20,6 +20,7 @@ Contents
                reference consumes its result as ``expert_offsets``.
 ``brute``      Independent int64 / float64 brute force used to pin the two
                modules above on small inputs.
+``repack``     The offline weight repack to the MFMA order and back.
 ``layer_ref``  The MoE-layer steps around the GEMM that this build adds (no
                reference counterpart): per-token int8 quantization, router
                top-k, SiLU-gated product with requantization, top-k combine,

@@ -182,3 +182,48 @@ def test_moe_layer_stagewise_and_end_to_end(pkg, dev, name, E, H, I, topk, M):
     # end to end against the oracle chain
     ref, _ = layer_ref.moe_layer_ref(x, logits, *w13, *w2, topk)
     _close(out, ref, f"{name}: layer")
+
+
+# ---------------------------------------------------------------- weight repack
+
+@pytest.mark.parametrize("E,N,K", [(2, 3, 8), (3, 70, 200), (8, 2048, 1024), (1, 1, 24)])
+def test_repack_bit_exact_and_round_trip(pkg, dev, E, N, K):
+    from oracle import repack
+    g = torch.Generator().manual_seed(E * N + K)
+    w = torch.randint(0, 256, (E, N, K // 2), dtype=torch.int32, generator=g).to(torch.uint8)
+    m = pkg.repack_weights(w.to(dev))
+    assert np.array_equal(m.cpu().numpy(), repack.to_mfma(w.numpy()))
+    back = pkg.repack_weights(m, inverse=True)
+    assert torch.equal(back.cpu(), w)
+
+
+@pytest.mark.parametrize("gs,zero", [(128, "symmetric"), (128, "full"), (64, "uint4"), (256, "symmetric"),
+                                     (256, "full")])
+def test_fused_moe_repacked_is_bit_identical(pkg, dev, gs, zero):
+    """Same outputs, bit for bit, from the repacked weights on every row-block
+    kernel (16 / 32 / 64 / 128 rows) and both unpacking paths."""
+    wl = pkg.workloads
+    print(f"[repacked] gs={gs} zero={zero}", flush=True)
+    E, N, K, M, topk = 8, 512, 2048, 256, 2
+    w_q4, w_scale, w_zero = wl.make_weights(E, N, K, gs, seed=gs + 5, device=dev, zero=zero)
+    x_q, x_scale = wl.make_activations(M, K, seed=gs + 6, device=dev)
+    ids, tw = wl.make_routing(M, E, topk, "softmax", seed=gs + 7, device=dev)
+    w_m = pkg.repack_weights(w_q4)
+    for bm in (16, 32, 64, 128):
+        a = pkg.w4a8_fused_moe(x_q, x_scale, w_q4, w_scale, w_zero, ids, tw, group_size=gs, block_m=bm)
+        b = pkg.w4a8_fused_moe(x_q, x_scale, w_m, w_scale, w_zero, ids, tw, group_size=gs, block_m=bm,
+                               weight_layout="mfma")
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"gs={gs} zero={zero} block_m={bm}"
+
+
+def test_moe_layer_repacked_is_bit_identical(pkg, dev):
+    x, logits, w13, w2 = _layer_inputs(pkg, 8, 1024, 512, 32, seed=77)
+    w13d = [t.to(dev) for t in w13]
+    w2d = [t.to(dev) for t in w2]
+    a = pkg.w4a8_moe_layer(x.to(dev), logits.to(dev), *w13d, *w2d, topk=2)
+    w13m = [pkg.repack_weights(w13d[0]), w13d[1], w13d[2]]
+    w2m = [pkg.repack_weights(w2d[0]), w2d[1], w2d[2]]
+    b = pkg.w4a8_moe_layer(x.to(dev), logits.to(dev), *w13m, *w2m, topk=2, weight_layout="mfma")
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

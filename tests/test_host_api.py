@@ -100,6 +100,16 @@ def test_layer_entries_reject_bad_arguments_without_device_work(pkg):
     assert L.mw4a8_combine_topk(p, 64, 4, 2, 64, ctypes.c_void_p(4098), p, 64, None) == -1
 
 
+def test_repack_entry_rejects_bad_arguments(pkg):
+    from flagos_kernel_gen_amd import _lib
+    L = _lib.lib()
+    p, q = ctypes.c_void_p(4096), ctypes.c_void_p(8192)
+    assert L.mw4a8_repack_weights(p, q, 2, 4, 12, 0, None) == -1                      # K % 8
+    assert L.mw4a8_repack_weights(p, p, 2, 4, 16, 0, None) == -1                      # in place
+    assert L.mw4a8_repack_weights(ctypes.c_void_p(4100), q, 2, 4, 16, 0, None) == -1  # alignment
+    assert L.mw4a8_repack_weights(p, q, 0, 4, 16, 0, None) == 0                       # nothing to do
+
+
 def test_layer_wrappers_fail_loudly_on_cpu(pkg):
     x = torch.zeros(4, 64, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
@@ -112,6 +122,8 @@ def test_layer_wrappers_fail_loudly_on_cpu(pkg):
         pkg.combine_topk(x, 2)
     with pytest.raises(TypeError):
         pkg.quant_per_token(x.float())
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        pkg.repack_weights(torch.zeros(2, 4, 8, dtype=torch.uint8))
 
 
 def _cpu_args(M=4, E=2, N=32, K=256, gs=128):

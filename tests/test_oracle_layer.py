@@ -147,3 +147,30 @@ def test_layer_with_one_expert_per_token_is_the_down_gemm_of_the_up_gemm(pkg):
     hq, hs = layer_ref.silu_mul_quant_ref(h)
     y = task1_ref.fused_moe_ref(hq, hs, *w2, ids, torch.ones(M, 1), 128)
     assert torch.equal(out, y)
+
+
+# ---------------------------------------------------------------- weight repack
+
+def test_repack_round_trip_and_element_order():
+    from oracle import repack
+    g = torch.Generator().manual_seed(41)
+    w = torch.randint(0, 256, (3, 5, 64), dtype=torch.int32, generator=g).to(torch.uint8)
+    m = repack.to_mfma(w.numpy())
+    assert np.array_equal(repack.from_mfma(m), w.numpy())
+    # byte i of run r holds elements 8r+i and 8r+i+4 (reference unpack), flipped by 8
+    u = task1_ref.unpack_int4(w).numpy()
+    for e in range(3):
+        for n in range(5):
+            for r in range(16):
+                for i in range(4):
+                    byte = int(m[e, n, 4 * r + i])
+                    assert (byte & 0xF) ^ 8 == u[e, n, 8 * r + i]
+                    assert (byte >> 4) ^ 8 == u[e, n, 8 * r + i + 4]
+
+
+def test_repack_hand_worked_run():
+    from oracle import repack
+    # run elements 0..7 = 0,1,...,7 -> reference bytes 0x10 0x32 0x54 0x76
+    ref = np.array([[[0x10, 0x32, 0x54, 0x76]]], dtype=np.uint8)
+    # byte i = (i ^ 8) | ((i + 4) ^ 8) << 4 -> 0xC8 0xD9 0xEA 0xFB
+    assert repack.to_mfma(ref).tolist() == [[[0xC8, 0xD9, 0xEA, 0xFB]]]
