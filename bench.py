@@ -271,6 +271,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-MoE-layer measurements")
+    ap.add_argument("--layers", default=",".join(p.split(":")[1] for p in LAYER_POINTS),
+                    help="token counts of the DeepSeek-V3 MoE-layer measurements (comma list)")
+    ap.add_argument("--layer-only", action="store_true",
+                    help="measure only the MoE layers (profiling; prints their JSON, not the bench line)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB int32 read+write kernel (torch.neg) to calibrate "
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE against known bytes")
@@ -286,6 +290,11 @@ def main():
     import __graft_entry__
     pkg = __graft_entry__.import_package()
     dev = torch.device("cuda:0")
+
+    if args.layer_only:
+        layers = [measure_layer(pkg, int(m), dev, args.steps, args.warmup) for m in args.layers.split(",")]
+        print(json.dumps({"layers": layers}), flush=True)
+        return
 
     head_name, head_m = HEADLINE
     if args.workload:
@@ -325,8 +334,7 @@ def main():
 
     layers = []
     if not args.headline_only and not args.no_layer:
-        for item in LAYER_POINTS:
-            M = int(item.split(":")[1])
+        for M in (int(m) for m in args.layers.split(",")):
             log(f"layer dsv3 M={M}")
             layers.append(measure_layer(pkg, M, dev, max(args.steps, 20), args.warmup))
             log(json.dumps(layers[-1]))
