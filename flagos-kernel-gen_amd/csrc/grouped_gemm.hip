@@ -50,11 +50,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcFlags);
 }
 
-// KCG consecutive int8 zero points at byte offset `off` (KCG-aligned) into
-// dst[g * stride + idx], sign-extended.
-template <int KCG, int NB>
-__device__ __forceinline__ void load_zero_run(__amdgpu_buffer_rsrc_t r, uint32_t off, int (&dst)[KCG][NB], int nb) {
-  uint32_t w[(KCG + 3) / 4];
+// KCG consecutive int8 zero points at byte offset `off` (KCG-aligned), kept
+// as raw words (zero point g is byte g % 4 of w[g / 4]). They are
+// sign-extended where they are used (zero_of), not here: extracting them
+// right after the load would make the wave wait for the load, and with it
+// for every load issued before it.
+template <int KCG>
+__device__ __forceinline__ void load_zero_run(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t (&w)[(KCG + 3) / 4]) {
   if constexpr (KCG == 1) {
     w[0] = __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
   } else if constexpr (KCG == 2) {
@@ -76,8 +78,11 @@ __device__ __forceinline__ void load_zero_run(__amdgpu_buffer_rsrc_t r, uint32_t
       w[4 * h + 3] = q.w;
     }
   }
-#pragma unroll
-  for (int g = 0; g < KCG; ++g) dst[g][nb] = (int)(int8_t)((w[g / 4] >> (8 * (g % 4))) & 0xffu);
+}
+
+template <int KCG>
+__device__ __forceinline__ int zero_of(const uint32_t (&w)[(KCG + 3) / 4], int g) {
+  return (int)(int8_t)((w[g / 4] >> (8 * (g % 4))) & 0xffu);
 }
 
 // KCG consecutive fp32 scales at byte offset `off` (4*KCG-aligned up to 16).
@@ -146,6 +151,11 @@ __device__ __forceinline__ int unit_pos(int cu) {
   return 16 * (g * UG + (v % S) * 4 + v / S);
 }
 
+// Chunks per zero-point/scale window (ZSV): the window's runs are read with
+// one vector load each per column block. RD chunks (the loop's unroll) while
+// the window's scales fit in 8 registers, else one chunk.
+__host__ __device__ constexpr int zs_window(int kcg, int rd) { return kcg * rd <= 8 ? rd : 1; }
+
 // Per-tile values shared by the kernel's setup and its tile bodies.
 struct TileCtx {
   int e;          // expert
@@ -169,7 +179,19 @@ struct TileCtx {
 //     zero-point / scale runs are aligned; the loop then carries no guards.
 //     (Used for the 16- and 32-row tiles only: without the guards the
 //     compiler schedules the larger bodies into scratch.)
-template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST>
+// ZSV (ZSG == 0 only): the zero points and scales of a window of
+//     zs_window(KCG, RD) chunks are read as one aligned vector run each per
+//     column (host-checked: G a multiple of the window's groups, 16-byte
+//     aligned tensors); otherwise one scalar load per group and chunk. Every
+//     such load costs the memory pipeline about as much as a 1 KB weight
+//     load (each touches one cache line per column), so fewer, wider runs
+//     leave more of it to the weights. It is a compile-time choice so that
+//     the loads of the next chunk lie on one straight path: with a run-time
+//     choice the compiler copied the loaded registers where the two paths
+//     join, and waited there for every outstanding load, which serialized
+//     the prefetch with the compute.
+template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST,
+          bool ZSV>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, int8_t* s_x, float* s_scale,
                                           int8_t* s_zero, const int* s_src, const int* s_dst, const float* s_xs,
                                           const float* s_tw) {
@@ -283,8 +305,23 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 
   struct WChunk {
     uint32_t w[KCG][NB][WD];
-    int z[KCG][NB];
-    float s[KCG][NB];
+    int z[KCG][NB];     // !ZSV: sign-extended zero points
+    float s[KCG][NB];   // !ZSV: scales
+  };
+  // ZSV: one window of ZW chunks (KW groups) of zero points (raw runs) and scales
+  constexpr int ZW = zs_window(KCG, RD);
+  constexpr int KW = ZW * KCG;
+  struct ZsWin {
+    uint32_t zr[NB][(KW + 3) / 4];
+    float s[KW][NB];
+  };
+  auto load_zs = [&](int win, ZsWin& d) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const uint32_t zo = zs_off[nb] + (uint32_t)(win * KW);
+      load_zero_run<KW>(z_rsrc, zo, d.zr[nb]);
+      if constexpr (!DEBUGP) load_scale_run<KW, NB>(s_rsrc, zo * 4u, d.s, nb);
+    }
   };
   auto load_w = [&](int ch, WChunk& d) {
 #pragma unroll
@@ -307,21 +344,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
             d.w[g][nb][4 * h + 3] = q.w;
           }
         }
-        if (!ZS_LDS && !FAST && !a.zs_vec) {
+        if constexpr (!ZS_LDS && !ZSV) {
           d.z[g][nb] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(z_rsrc, zs_off[nb] + gg, 0, 0);
           if constexpr (!DEBUGP)
             d.s[g][nb] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(s_rsrc, (zs_off[nb] + gg) * 4u, 0, 0));
         }
-      }
-    }
-    if (!ZS_LDS && (FAST || a.zs_vec)) {
-      // the chunk's KCG zero points and scales of a column are contiguous:
-      // one or two vector loads per column instead of 2 * KCG scalar loads
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const uint32_t zo = zs_off[nb] + (uint32_t)(ch * KCG);
-        load_zero_run<KCG, NB>(z_rsrc, zo, d.z, nb);
-        if constexpr (!DEBUGP) load_scale_run<KCG, NB>(s_rsrc, zo * 4u, d.s, nb);
       }
     }
   };
@@ -335,7 +362,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       for (int r = 0; r < 4; ++r) acc[mb][nb][r] = 0.f;
 
   // ---- one chunk of K ------------------------------------------------------
-  auto compute = [&](int ch, const int8_t* xb, const WChunk& wc) {
+  // dd: position of the chunk in its zero/scale window (compile-time after unrolling)
+  auto compute = [&](int ch, const int8_t* xb, const WChunk& wc, const ZsWin& zw, int dd) {
 #pragma unroll
     for (int g = 0; g < KCG; ++g) {
       const int gg = ch * KCG + g;
@@ -347,6 +375,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
           if constexpr (ZS_LDS) {
             zv[nb] = s_zero[zs_lds[nb] + gg];
             sv[nb] = s_scale[zs_lds[nb] + gg];
+          } else if constexpr (ZSV) {
+            zv[nb] = zero_of<KW>(zw.zr[nb], dd * KCG + g);
+            sv[nb] = zw.s[dd * KCG + g][nb];
           } else {
             zv[nb] = wc.z[g][nb];
             sv[nb] = wc.s[g][nb];
@@ -447,11 +478,20 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   };
 
   // ---- main loop: chunk c uses ring slot c % RD ----------------------------
+  // Next-chunk loads are issued unconditionally; past the end the chunk
+  // index is clamped to the last chunk (loaded again, never used), so no
+  // branch surrounds a load and no join makes the compiler wait for one.
+  const int last_chunk = c.nchunks - 1;
+  const int last_win = (c.nchunks + ZW - 1) / ZW - 1;
   WChunk ring[RD];
+  // zs_cur serves the current window; zs_next is loaded one window ahead and
+  // copied in at each window start (after the activation wait, which has
+  // covered its load: it was issued before those activations)
+  ZsWin zs_cur, zs_next;
+  if constexpr (!ZS_LDS && ZSV) load_zs(0, zs_next);
   load_x(0);
 #pragma unroll
-  for (int d = 0; d < RD - 1; ++d)
-    if (d < c.nchunks) load_w(d, ring[d]);
+  for (int d = 0; d < RD - 1; ++d) load_w(min(d, last_chunk), ring[d]);
   if constexpr (ZS_LDS) {
     // visible to all waves after the first barrier of the loop
 #pragma unroll
@@ -472,9 +512,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       if (FAST || cc < c.nchunks) {
         store_x(cc & 1);
         __syncthreads();
-        if (cc + 1 < c.nchunks) load_x(cc + 1);
-        if (cc + RD - 1 < c.nchunks) load_w(cc + RD - 1, ring[(d + RD - 1) % RD]);
-        compute(cc, s_x + (cc & 1) * BUF, ring[d]);
+        if constexpr (!ZS_LDS && ZSV) {
+          if (d % ZW == 0) {
+            zs_cur = zs_next;
+            load_zs(min(cc / ZW + 1, last_win), zs_next);
+          }
+        }
+        load_x(min(cc + 1, last_chunk));
+        load_w(min(cc + RD - 1, last_chunk), ring[(d + RD - 1) % RD]);
+        compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
       }
     }
   }
@@ -501,7 +547,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 
 // ZSG > 0: zero points and scales come from an LDS copy of the tile's
 // block; the host launches this only when G <= ZSG (see zs_block_fits).
-template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST,
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST, bool ZSV,
           int WAVES_PER_EU>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU)))
 void w4a8_gemm_kernel(const GemmArgs a) {
@@ -593,12 +639,13 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   // tiles whose valid rows fit in the top half run the half-height body
   if constexpr (BM >= 64) {
     if (rows <= BM / 2) {
-      gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST>(a, c, s_x, s_scale, s_zero, s_src, s_dst,
+      gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV>(a, c, s_x, s_scale, s_zero, s_src, s_dst,
                                                                      s_xs, s_tw);
       return;
     }
   }
-  gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST>(a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs, s_tw);
+  gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV>(a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs,
+                                                                        s_tw);
 }
 
 // ---------------------------------------------------------------------------
@@ -622,20 +669,26 @@ static bool zs_block_fits(const GemmArgs& a, int BN, int ZSG) {
 template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, int WPE>
 static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   set_grid(a, max_blocks, NW * WN, R);
-  // a column's KCG zero points / scales of one chunk can be read as one
-  // aligned run when G is a multiple of KCG and both tensors are 16-byte aligned
-  a.zs_vec = (a.G % KCG == 0) && (reinterpret_cast<uintptr_t>(a.wz) % 16 == 0) &&
+  // a column's zero points / scales of one window can be read as one aligned
+  // run when G is a multiple of the window's groups and both tensors are
+  // 16-byte aligned
+  a.zs_vec = (a.G % (KCG * zs_window(KCG, RD)) == 0) && (reinterpret_cast<uintptr_t>(a.wz) % 16 == 0) &&
              (reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
   if (a.total_tiles == 0) return hipSuccess;
   // the guard-free body needs whole chunks, a chunk count divisible by the
   // unroll, and (without the LDS zero/scale block) aligned vector runs
   constexpr bool CAN_FAST = !DEBUGP && BM <= 32;
+  constexpr bool RUNS = ZSG == 0 && !DEBUGP;   // vector zero/scale runs apply
+  const dim3 grid(8 * a.per_xcd), block(NW * 64);
   if (CAN_FAST && a.G % (KCG * RD) == 0 && (ZSG > 0 || a.zs_vec))
-    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, CAN_FAST, WPE>),
-                       dim3(8 * a.per_xcd), dim3(NW * 64), 0, s, a);
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, CAN_FAST, RUNS, WPE>), grid,
+                       block, 0, s, a);
+  else if (RUNS && a.zs_vec)
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, RUNS, WPE>), grid, block,
+                       0, s, a);
   else
-    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, WPE>),
-                       dim3(8 * a.per_xcd), dim3(NW * 64), 0, s, a);
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, false, WPE>), grid, block,
+                       0, s, a);
   return hipGetLastError();
 }
 
