@@ -526,22 +526,65 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   }
 
   if constexpr (!DEBUGP) {
+    // 128-column tiles: the finished tile goes through LDS (the activation
+    // buffers are free now) so that every row leaves as 16-byte stores of
+    // its 256 contiguous bytes -- 8 store instructions per wave instead of 64
+    // two-byte ones (an MFMA lane holds four rows of one column). Row r's
+    // 16-byte segment s sits at r * 256 + 16 * (s ^ (r % 16)): the four rows
+    // of one ds_write_b16 hit distinct segments, and so do the two rows of a
+    // ds_read_b128 half-wave (opposite parity: disjoint bank halves).
+    constexpr bool TILE_OUT = BN == 128 && BM >= 64;
+    bool stored = false;
+    if constexpr (TILE_OUT) {
+      if (a.vec_out) {
+        uint8_t* tile = reinterpret_cast<uint8_t*>(s_x);
+        __syncthreads();   // every wave has finished reading the activation buffers
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int col = c.col0 + nb * 16 + jl;
+          for (int nb = 0; nb < NB; ++nb) {
+            const int cl = c.col0 - c.tile_col0 + nb * 16 + jl;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = mb * 16 + kb * 4 + r;
+            for (int r = 0; r < 4; ++r) {
+              const int row = mb * 16 + kb * 4 + r;
+              float v = acc[mb][nb][r] * s_xs[row];
+              if constexpr (ROUTED) v = v * s_tw[row];
+              const int off = row * 256 + (((cl >> 3) ^ (row & 15)) << 4) + ((cl & 7) << 1);
+              *reinterpret_cast<uint16_t*>(tile + off) = bf16_rne_bits(__float_as_uint(v));
+            }
+          }
+        __syncthreads();
+        static_assert((BMX * 16) % NT == 0, "output rounds");
+#pragma unroll
+        for (int i = 0; i < BMX * 16 / NT; ++i) {
+          const int t = tid + i * NT;
+          const int row = t >> 4, seg = t & 15;
+          const u32x4 v = *reinterpret_cast<const u32x4*>(tile + row * 256 + ((seg ^ (row & 15)) << 4));
           const int dst = s_dst[row];
-          if (dst >= 0 && col < a.N) {
-            float v = acc[mb][nb][r] * s_xs[row];
-            if constexpr (ROUTED) v = v * s_tw[row];
-            a.out[(int64_t)dst * a.ldo + col] = bf16_rne_bits(__float_as_uint(v));
+          const int col = c.tile_col0 + seg * 8;
+          if (dst >= 0 && col < a.N) *reinterpret_cast<u32x4*>(a.out + (int64_t)dst * a.ldo + col) = v;
+        }
+        stored = true;
+      }
+    }
+    if (!stored) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int col = c.col0 + nb * 16 + jl;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = mb * 16 + kb * 4 + r;
+            const int dst = s_dst[row];
+            if (dst >= 0 && col < a.N) {
+              float v = acc[mb][nb][r] * s_xs[row];
+              if constexpr (ROUTED) v = v * s_tw[row];
+              a.out[(int64_t)dst * a.ldo + col] = bf16_rne_bits(__float_as_uint(v));
+            }
           }
         }
-      }
+    }
   }
 }
 
@@ -674,6 +717,8 @@ static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   // 16-byte aligned
   a.zs_vec = (a.G % (KCG * zs_window(KCG, RD)) == 0) && (reinterpret_cast<uintptr_t>(a.wz) % 16 == 0) &&
              (reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
+  // output rows can be written in 16-byte pieces
+  a.vec_out = (a.N % 8 == 0) && (a.ldo % 8 == 0) && (reinterpret_cast<uintptr_t>(a.out) % 16 == 0);
   if (a.total_tiles == 0) return hipSuccess;
   // the guard-free body needs whole chunks, a chunk count divisible by the
   // unroll, and (without the LDS zero/scale block) aligned vector runs

@@ -35,6 +35,7 @@ struct GemmArgs {
   int32_t* dbg;               // debug partials [rows, N, G] (debug kernels only)
   int N, K, G;
   int zs_vec;                 // zero points/scales of a K-chunk load as one vector run per column
+  int vec_out;                // output rows may be stored in 16-byte pieces (N, ldo multiples of 8; aligned)
   // launch geometry (see grid_for)
   int n_tiles, R, total_tiles, per_xcd;
 };

@@ -189,6 +189,30 @@ def test_grouped_scale_zero_fallback_paths(pkg, dev, case):
     assert_close(out, ref, N, case)
 
 
+@pytest.mark.parametrize("N,pad,K", [(1004, 0, 768), (512, 8, 768), (512, 4, 768), (384, 8, 4608)])
+def test_grouped_output_store_paths(pkg, dev, N, pad, K):
+    """64/128-row tiles store rows in 16-byte pieces through LDS when N and
+    the row stride of ``out`` are multiples of 8, element by element
+    otherwise: N = 1004, a stride of N + 4 (element path) and of N + 8
+    (16-byte path, stride != N), on 64-row (K = 768) and 128-row (K = 4608)
+    tiles. Columns past N in the padded rows stay untouched."""
+    wl = pkg.workloads
+    E, rows = 3, 200
+    print(f"[store] N={N} pad={pad} K={K}", flush=True)
+    x_q, x_scale, w_q4, w_scale, w_zero, offs = wl.make_grouped_inputs(E, rows * E, N, K, 128, seed=N + pad + K)
+    M = rows * E
+    ref = task1_ref.w4a8_group_gemm_moe_ref(x_q, x_scale, w_q4, w_scale, w_zero, offs,
+                                            torch.zeros(M, N, dtype=torch.bfloat16), 128)
+    big = torch.full((M, N + pad), 7.0, dtype=torch.bfloat16, device=dev)
+    out = big[:, :N]
+    pkg.w4a8_group_gemm_moe(x_q.to(dev), x_scale.to(dev), w_q4.to(dev), w_scale.to(dev), w_zero.to(dev),
+                            offs.to(dev), out, 128)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), ref, N, f"store N={N} pad={pad} K={K}")
+    if pad:
+        assert bool((big[:, N:] == 7.0).all()), "columns past N were written"
+
+
 @pytest.mark.parametrize("rows_per_expert", [8, 24, 60, 200])
 def test_grouped_every_block_size(pkg, dev, rows_per_expert):
     """Row counts that select each of the 16/32/64/128 row-block kernels."""
