@@ -478,9 +478,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   };
 
   // ---- main loop: chunk c uses ring slot c % RD ----------------------------
-  // Next-chunk loads are issued unconditionally; past the end the chunk
-  // index is clamped to the last chunk (loaded again, never used), so no
-  // branch surrounds a load and no join makes the compiler wait for one.
+  // 64/128-row tiles issue the next chunk's loads unconditionally, past the
+  // end with the chunk index clamped to the last chunk (loaded again, never
+  // used): no branch surrounds a load, so no join makes the compiler wait for
+  // one (which serialized their prefetch). The 16/32-row tiles run a few
+  // chunks per tile, where the extra chunk costs more than the join (measured
+  // on the decode points), so they skip the loads past the end.
+  constexpr bool CLAMP = BM >= 64;
   const int last_chunk = c.nchunks - 1;
   const int last_win = (c.nchunks + ZW - 1) / ZW - 1;
   WChunk ring[RD];
@@ -491,7 +495,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   if constexpr (!ZS_LDS && ZSV) load_zs(0, zs_next);
   load_x(0);
 #pragma unroll
-  for (int d = 0; d < RD - 1; ++d) load_w(min(d, last_chunk), ring[d]);
+  for (int d = 0; d < RD - 1; ++d) {
+    if constexpr (CLAMP) {
+      load_w(min(d, last_chunk), ring[d]);
+    } else {
+      if (d < c.nchunks) load_w(d, ring[d]);
+    }
+  }
   if constexpr (ZS_LDS) {
     // visible to all waves after the first barrier of the loop
 #pragma unroll
@@ -515,11 +525,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         if constexpr (!ZS_LDS && ZSV) {
           if (d % ZW == 0) {
             zs_cur = zs_next;
-            load_zs(min(cc / ZW + 1, last_win), zs_next);
+            if (CLAMP || cc / ZW + 1 <= last_win) load_zs(min(cc / ZW + 1, last_win), zs_next);
           }
         }
-        load_x(min(cc + 1, last_chunk));
-        load_w(min(cc + RD - 1, last_chunk), ring[(d + RD - 1) % RD]);
+        if constexpr (CLAMP) {
+          load_x(min(cc + 1, last_chunk));
+          load_w(min(cc + RD - 1, last_chunk), ring[(d + RD - 1) % RD]);
+        } else {
+          if (cc + 1 < c.nchunks) load_x(cc + 1);
+          if (cc + RD - 1 < c.nchunks) load_w(cc + RD - 1, ring[(d + RD - 1) % RD]);
+        }
         compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
       }
     }
