@@ -34,6 +34,8 @@
 // (usually of one expert) across all column tiles before moving on, so the
 // activation rows and the weight tile a row block pair shares stay in that
 // XCD's L2.
+#include <type_traits>
+
 #include "mw4a8_internal.h"
 #include "mw4a8_pack.h"
 
@@ -515,7 +517,60 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       if (u < z_units) *reinterpret_cast<u32x4*>(s_zero + 16 * u) = zq[j];
     }
   }
-  for (int ch = 0; ch < c.nchunks; ch += RD) {
+  // STAGGER (8-wave 256-column tiles): half of the waves run the chunk
+  // interval in the opposite order, so that the CU's load bursts and compute
+  // phases overlap: early waves loads(c+1), compute(c), store A(c+1); late
+  // waves compute(c), store A(c+1) (loaded one interval earlier), loads(c+2) --
+  // into the weight slot compute(c) has just finished with. One barrier per
+  // chunk for all waves, as in the plain loop. Waves are placed round-robin
+  // (w and w + 4 share a SIMD); of the groupings measured, late = waves 2, 3,
+  // 6, 7 (each SIMD's two waves in the same order, two SIMDs each way) was
+  // fastest -- faster than the SIMD mates in opposite orders.
+  constexpr bool STAGGER = NW == 8 && BMX == BM && RD == 2 && CLAMP;
+  if constexpr (STAGGER) {
+    // one interval of chunk cc (ring parity d); LATE selects the order
+    auto interval = [&](int cc, int d, auto late_tag) {
+      constexpr bool LATE = decltype(late_tag)::value;
+      if constexpr (!ZS_LDS && ZSV) {
+        if (d % ZW == 0) {
+          zs_cur = zs_next;
+          load_zs(min(cc / ZW + 1, last_win), zs_next);
+        }
+      }
+      if constexpr (LATE) {
+        compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
+        store_x((cc + 1) & 1);
+        load_x(min(cc + 2, last_chunk));
+        load_w(min(cc + 2, last_chunk), ring[d]);
+      } else {
+        load_x(min(cc + 1, last_chunk));
+        load_w(min(cc + 1, last_chunk), ring[(d + 1) % 2]);
+        compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
+        store_x((cc + 1) & 1);
+      }
+      __syncthreads();
+    };
+    // two separate loops (no join inside either, so no waits for loads there)
+    if (((tid >> 6) >> 1) & 1) {
+      // one more chunk in flight: A(1) in registers, W(1) in the ring
+      store_x(0);
+      load_x(min(1, last_chunk));
+      load_w(min(1, last_chunk), ring[1]);
+      __syncthreads();
+      for (int ch = 0; ch < c.nchunks; ch += 2) {
+        interval(ch, 0, std::true_type{});
+        if (ch + 1 < c.nchunks) interval(ch + 1, 1, std::true_type{});
+      }
+    } else {
+      store_x(0);
+      __syncthreads();
+      for (int ch = 0; ch < c.nchunks; ch += 2) {
+        interval(ch, 0, std::false_type{});
+        if (ch + 1 < c.nchunks) interval(ch + 1, 1, std::false_type{});
+      }
+    }
+  }
+  for (int ch = 0; ch < (STAGGER ? 0 : c.nchunks); ch += RD) {
 #pragma unroll
     for (int d = 0; d < RD; ++d) {
       const int cc = ch + d;
@@ -548,7 +603,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     // 16-byte segment s sits at r * 256 + 16 * (s ^ (r % 16)): the four rows
     // of one ds_write_b16 hit distinct segments, and so do the two rows of a
     // ds_read_b128 half-wave (opposite parity: disjoint bank halves).
-    constexpr bool TILE_OUT = BN == 128 && BM >= 64;
+    constexpr bool TILE_OUT = (BN == 128 || BN == 256) && BM >= 64;
+    constexpr int SEG = BN / 8;          // 16-byte segments per tile row
+    constexpr int ROWB = BN * 2;         // bytes per tile row
     bool stored = false;
     if constexpr (TILE_OUT) {
       if (a.vec_out) {
@@ -564,17 +621,17 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
               const int row = mb * 16 + kb * 4 + r;
               float v = acc[mb][nb][r] * s_xs[row];
               if constexpr (ROUTED) v = v * s_tw[row];
-              const int off = row * 256 + (((cl >> 3) ^ (row & 15)) << 4) + ((cl & 7) << 1);
+              const int off = row * ROWB + (((cl >> 3) ^ (row & (SEG - 1))) << 4) + ((cl & 7) << 1);
               *reinterpret_cast<uint16_t*>(tile + off) = bf16_rne_bits(__float_as_uint(v));
             }
           }
         __syncthreads();
-        static_assert((BMX * 16) % NT == 0, "output rounds");
+        static_assert((BMX * SEG) % NT == 0, "output rounds");
 #pragma unroll
-        for (int i = 0; i < BMX * 16 / NT; ++i) {
+        for (int i = 0; i < BMX * SEG / NT; ++i) {
           const int t = tid + i * NT;
-          const int row = t >> 4, seg = t & 15;
-          const u32x4 v = *reinterpret_cast<const u32x4*>(tile + row * 256 + ((seg ^ (row & 15)) << 4));
+          const int row = t / SEG, seg = t % SEG;
+          const u32x4 v = *reinterpret_cast<const u32x4*>(tile + row * ROWB + ((seg ^ (row & (SEG - 1))) << 4));
           const int dst = s_dst[row];
           const int col = c.tile_col0 + seg * 8;
           if (dst >= 0 && col < a.N) *reinterpret_cast<u32x4*>(a.out + (int64_t)dst * a.ldo + col) = v;
@@ -769,7 +826,12 @@ static hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, h
       return launch_one<32, 16, 4, GS, K512, 2, 0, RMODE, false, 1>(a, max_blocks, c.R, s);
     // three waves per SIMD fit the gs = 128 body without spills; the others keep two
     case 64: return launch_one<64, 32, 4, GS, K256, 2, 0, RMODE, false, GS == 128 ? 3 : 2>(a, max_blocks, c.R, s);
-    case 128: return launch_one<128, 32, 4, GS, K256, 2, 0, RMODE, false, 2>(a, max_blocks, c.R, s);
+    case 128:
+      // group size 128: 8 waves x 32 columns, staggered (see STAGGER)
+      if constexpr (GS == 128)
+        return launch_one<128, 32, 8, GS, K256, 2, 0, RMODE, false, 2>(a, max_blocks, c.R, s);
+      else
+        return launch_one<128, 32, 4, GS, K256, 2, 0, RMODE, false, 2>(a, max_blocks, c.R, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -814,7 +876,7 @@ TileConfig tiles_for_block_m(int BM, int group_size) {
     case 16: c.WN = 16; c.KCG = 512 / group_size; c.R = 1; break;
     case 32: c.WN = 16; c.KCG = 512 / group_size; c.R = 1; break;
     case 64: c.WN = 32; c.KCG = 256 / group_size; c.R = 2; break;
-    default: c.BM = 128; c.WN = 32; c.KCG = 256 / group_size; c.R = 2; break;
+    default: c.BM = 128; c.WN = 32; c.KCG = 256 / group_size; c.R = 2; c.NW = group_size == 128 ? 8 : 4; break;
   }
   if (c.KCG < 1) c.KCG = 1;
   return c;
