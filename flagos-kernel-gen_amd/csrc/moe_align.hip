@@ -16,6 +16,16 @@
 //      the output bit-exact with a stable sort. No workgroup barrier is
 //      needed after the scan.
 //
+// moe_align_split_kernel: the same result from NB workgroups, for larger
+//   pair counts (one workgroup's scattered stores were the bottleneck).
+//   Every workgroup reads all the ids (they are small and stay in L2) and
+//   counts, per expert, the pairs before its own segment and from it on; the
+//   totals give every workgroup the same padded layout, the counts before the
+//   segment its own starting slot per expert. It then scatters only its own
+//   segment exactly as above, so the slot of a pair is the same as with one
+//   workgroup. Padding slots, expert_ids and the tails are split over the
+//   workgroups by expert and by slot. No workgroup depends on another.
+//
 // csr_block_table_kernel: CSR expert_offsets (reference layout,
 //   docs/Task1.md:87-92) -> list of (expert, first row, end row) blocks of
 //   at most BM rows, so the GEMM grid needs no host-side count.
@@ -166,13 +176,138 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   }
 }
 
+__global__ __launch_bounds__(kAlignThreads) void moe_align_split_kernel(
+    const int32_t* __restrict__ topk_ids, int P, int E, int BM, int id_bits,
+    int32_t* __restrict__ sorted_ids, int sorted_len,
+    int32_t* __restrict__ expert_ids, int blocks_len,
+    int32_t* __restrict__ num_post_pad, int32_t* __restrict__ expert_offsets) {
+  // per-wave counts of this segment; after the scan, each wave's next free slot
+  __shared__ int s_wcnt[kAlignWaves][kAlignMaxE];
+  __shared__ int s_pre[kAlignMaxE];    // pairs before the segment, per expert
+  __shared__ int s_post[kAlignMaxE];   // pairs from the segment on, per expert
+  __shared__ int s_wave[kAlignWaves];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nb = gridDim.x, b = blockIdx.x;
+
+  for (int i = tid; i < kAlignWaves * kAlignMaxE; i += kAlignThreads) (&s_wcnt[0][0])[i] = 0;
+  for (int i = tid; i < kAlignMaxE; i += kAlignThreads) {
+    s_pre[i] = 0;
+    s_post[i] = 0;
+  }
+  __syncthreads();
+
+  // this workgroup's segment [s0, s1); wave w owns [p0, p1) of it
+  const int seg = (P + nb - 1) / nb;
+  const int s0 = min(P, b * seg);
+  const int s1 = min(P, s0 + seg);
+  const int wseg = (s1 - s0 + kAlignWaves - 1) / kAlignWaves;
+  const int p0 = min(s1, s0 + wave * wseg);
+  const int p1 = min(s1, p0 + wseg);
+
+  // 1. counts over all pairs: before the segment, from it on, and per owning
+  //    wave inside it
+  constexpr int kBatch = 8;
+  for (int i0 = tid; i0 < P; i0 += kAlignThreads * kBatch) {
+    int ev[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int i = i0 + kAlignThreads * j;
+      ev[j] = i < P ? topk_ids[i] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int i = i0 + kAlignThreads * j;
+      if ((unsigned)ev[j] < (unsigned)E) {
+        atomicAdd(i < s0 ? &s_pre[ev[j]] : &s_post[ev[j]], 1);
+        if (i >= s0 && i < s1) atomicAdd(&s_wcnt[min((i - s0) / wseg, kAlignWaves - 1)][ev[j]], 1);
+      }
+    }
+  }
+  __syncthreads();
+
+  // 2. the padded layout (identical in every workgroup) and this segment's
+  //    per-wave starting slots
+  int my_cnt = 0, my_pre = 0;
+  if (tid < E) {
+    my_pre = s_pre[tid];
+    my_cnt = my_pre + s_post[tid];
+  }
+  const int my_blk = (my_cnt + BM - 1) / BM;
+  int tot_blk, tot_cnt;
+  const int blk_ex = block_exclusive_scan(my_blk, s_wave, &tot_blk);
+  const int cnt_ex = block_exclusive_scan(my_cnt, s_wave, &tot_cnt);
+  if (tid < E) {
+    int run = blk_ex * BM + my_pre;
+#pragma unroll
+    for (int w = 0; w < kAlignWaves; ++w) {
+      const int cnt = s_wcnt[w][tid];
+      s_wcnt[w][tid] = run;
+      run += cnt;
+    }
+    // expert tid's padding, block ids and offset: written by one workgroup
+    if (tid % nb == b) {
+      if (expert_offsets) expert_offsets[tid] = cnt_ex;
+      const int first = blk_ex * BM;
+      for (int sl = first + my_cnt; sl < first + my_blk * BM; ++sl) sorted_ids[sl] = P;
+      for (int bb = blk_ex; bb < blk_ex + my_blk; ++bb) expert_ids[bb] = tid;
+    }
+  }
+  if (b == 0 && tid == 0) {
+    if (expert_offsets) expert_offsets[E] = tot_cnt;
+    num_post_pad[0] = tot_blk * BM;
+  }
+  for (int sl = tot_blk * BM + b * kAlignThreads + tid; sl < sorted_len; sl += nb * kAlignThreads) sorted_ids[sl] = P;
+  for (int bb = tot_blk + b * kAlignThreads + tid; bb < blocks_len; bb += nb * kAlignThreads) expert_ids[bb] = -1;
+  __syncthreads();
+
+  // 3. stable scatter of the segment (as in moe_align_kernel)
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int base = p0; base < p1; base += 64) {
+    const int i = base + lane;
+    const int e = i < p1 ? topk_ids[i] : -1;
+    const bool valid = (unsigned)e < (unsigned)E;
+    uint64_t peers = __ballot(valid);
+    for (int bit = 0; bit < id_bits; ++bit) {
+      const bool set = (e >> bit) & 1;
+      const uint64_t m = __ballot(set);
+      peers &= set ? m : ~m;
+    }
+    const int rank = __popcll(peers & lt_mask);
+    const int count = __popcll(peers);
+    int slot = 0;
+    if (valid) slot = s_wcnt[wave][e] + rank;
+    __builtin_amdgcn_wave_barrier();
+    if (valid) {
+      sorted_ids[slot] = i;
+      if (rank == 0) s_wcnt[wave][e] = slot + count;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// Workgroups for the split kernel: one per ~1024 pairs, at most 64 (every
+// workgroup reads all ids: 64 x the id array of L2 traffic at most).
+int align_workgroups(int num_pairs) {
+  if (num_pairs < 4096) return 1;
+  const int nb = (num_pairs + 1023) / 1024;
+  return nb < 64 ? nb : 64;
+}
+
 hipError_t launch_moe_align(const int32_t* topk_ids, int num_pairs, int E, int BM,
                             int32_t* sorted_ids, int sorted_len, int32_t* expert_ids, int blocks_len,
                             int32_t* num_post_pad, int32_t* expert_offsets, hipStream_t s) {
   int id_bits = 0;
   while ((1 << id_bits) < E) ++id_bits;
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, s, topk_ids, num_pairs, E, BM,
-                     id_bits, sorted_ids, sorted_len, expert_ids, blocks_len, num_post_pad, expert_offsets);
+  const int nb = align_workgroups(num_pairs);
+  if (nb > 1)
+    hipLaunchKernelGGL(moe_align_split_kernel, dim3(nb), dim3(kAlignThreads), 0, s, topk_ids, num_pairs, E, BM,
+                       id_bits, sorted_ids, sorted_len, expert_ids, blocks_len, num_post_pad, expert_offsets);
+  else
+    hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, s, topk_ids, num_pairs, E, BM,
+                       id_bits, sorted_ids, sorted_len, expert_ids, blocks_len, num_post_pad, expert_offsets);
   return hipGetLastError();
 }
 
