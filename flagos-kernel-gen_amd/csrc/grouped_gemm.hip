@@ -828,9 +828,13 @@ static hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, h
     case 64: return launch_one<64, 32, 4, GS, K256, 2, 0, RMODE, false, GS == 128 ? 3 : 2>(a, max_blocks, c.R, s);
     case 128:
       // group size 128: 8 waves x 32 columns, staggered (see STAGGER)
-      if constexpr (GS == 128)
+      if constexpr (GS == 128) {
+        // the tile's whole [256 x G] zero-point/scale block in LDS when G <= 64
+        // (80 KB beside the 72 KB of activation buffers: one tile per CU)
+        if (zs_block_fits(a, 256, 64))
+          return launch_one<128, 32, 8, GS, K256, 2, 64, RMODE, false, 2>(a, max_blocks, c.R, s);
         return launch_one<128, 32, 8, GS, K256, 2, 0, RMODE, false, 2>(a, max_blocks, c.R, s);
-      else
+      } else
         return launch_one<128, 32, 4, GS, K256, 2, 0, RMODE, false, 2>(a, max_blocks, c.R, s);
     default: return hipErrorInvalidValue;
   }
