@@ -825,7 +825,12 @@ static hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, h
       if (zs_block_fits(a, 64, 64)) return launch_one<32, 16, 4, GS, K512, 2, 64, RMODE, false, 1>(a, max_blocks, c.R, s);
       return launch_one<32, 16, 4, GS, K512, 2, 0, RMODE, false, 1>(a, max_blocks, c.R, s);
     // three waves per SIMD fit the gs = 128 body without spills; the others keep two
-    case 64: return launch_one<64, 32, 4, GS, K256, 2, 0, RMODE, false, GS == 128 ? 3 : 2>(a, max_blocks, c.R, s);
+    case 64:
+      // G <= 16 (K <= 2048 at group size 128): the tile's [128 x G] zero/scale
+      // block in LDS (10 KB; three workgroups per CU still fit)
+      if (zs_block_fits(a, 128, 16))
+        return launch_one<64, 32, 4, GS, K256, 2, 16, RMODE, false, GS == 128 ? 3 : 2>(a, max_blocks, c.R, s);
+      return launch_one<64, 32, 4, GS, K256, 2, 0, RMODE, false, GS == 128 ? 3 : 2>(a, max_blocks, c.R, s);
     case 128:
       // group size 128: 8 waves x 32 columns, staggered (see STAGGER)
       if constexpr (GS == 128) {
