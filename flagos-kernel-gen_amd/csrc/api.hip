@@ -398,6 +398,47 @@ int mw4a8_host_selftest(void) {
         got += (int64_t)(int8_t)((a[w] >> (8 * by)) & 0xff) * (int8_t)((bw[w] >> (8 * by)) & 0xff);
     bad += got != want;
   }
+  // expert-grouped tile order: over random expert runs (empty experts, runs
+  // of 1..12 blocks), every (block, column tile) is produced exactly once
+  // with the block's expert; groups stay inside one run, start at the run's
+  // first block plus a multiple of R and hold at most R blocks; the tiles of
+  // one group and column tile are consecutive in the list.
+  for (int trial = 0; trial < 300; ++trial) {
+    int32_t ids[160];
+    int nblocks = 0;
+    const int E = 1 + (int)(rnd() % 24);
+    for (int ex = 0; ex < E && nblocks < 148; ++ex) {
+      const int run = (rnd() % 4 == 0) ? 0 : 1 + (int)(rnd() % ((trial & 1) ? 12 : 3));
+      for (int j = 0; j < run && nblocks < 148; ++j) ids[nblocks++] = ex;
+    }
+    if (nblocks == 0) continue;
+    const int R = 1 + (int)(rnd() % 4);
+    const int n_tiles = 1 + (int)(rnd() % 7);
+    static uint8_t seen[160 * 8];
+    memset(seen, 0, sizeof(seen));
+    int prev_key = -1;
+    uint8_t key_done[160 * 8];
+    memset(key_done, 0, sizeof(key_done));
+    for (int t = 0; t < nblocks * n_tiles; ++t) {
+      int b = -1, nt = -1, ex = -1;
+      if (!expert_group_tile(t, n_tiles, R, nblocks, ids, E, b, nt, ex) || b < 0 || b >= nblocks ||
+          nt < 0 || nt >= n_tiles || ids[b] != ex) {
+        ++bad;
+        continue;
+      }
+      bad += seen[b * n_tiles + nt]++ != 0;
+      int first = b;   // run start, by walking back
+      while (first > 0 && ids[first - 1] == ex) --first;
+      const int g0 = first + (b - first) / R * R;
+      const int key = g0 * n_tiles + nt;   // (group, column tile)
+      if (key != prev_key) {
+        bad += key_done[key] != 0;   // a (group, column) seen before must not reappear
+        if (prev_key >= 0) key_done[prev_key] = 1;
+        prev_key = key;
+      }
+    }
+    for (int i = 0; i < nblocks * n_tiles; ++i) bad += seen[i] != 1;
+  }
   // bf16 round to nearest even
   struct Case { uint32_t in; uint16_t out; };
   const Case cases[] = {

@@ -695,26 +695,32 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   } else {
     nblocks = a.blk_count[0];
   }
+  // routed 64/128-row tiles may run in expert groups (the host decides)
+  const bool egroups = ROUTED && BM >= 64 && a.egroups;
   const int span = a.n_tiles * a.R;
-  const int tiles = (nblocks + a.R - 1) / a.R * span;
+  const int tiles = egroups ? nblocks * a.n_tiles : (nblocks + a.R - 1) / a.R * span;
   const int per_xcd = (tiles + 7) >> 3;
   const int L = blockIdx.x;
   if ((L >> 3) >= per_xcd) return;
   const int t = (L & 7) * per_xcd + (L >> 3);
   if (t >= tiles) return;
-  const int chunk_id = t / span;
-  const int rem = t - chunk_id * span;
-  const int nt = rem / a.R;
-  const int b = chunk_id * a.R + (rem - nt * a.R);
-  if (b >= nblocks) return;
-  int e;
-  if constexpr (ROUTED) {
-    e = a.expert_ids[b];
-    if (e >= a.E) return;
+  int b, nt, e;
+  if (egroups) {
+    if (!expert_group_tile(t, a.n_tiles, a.R, nblocks, a.expert_ids, a.E, b, nt, e)) return;
   } else {
-    e = a.blk_expert[b];
+    const int chunk_id = t / span;
+    const int rem = t - chunk_id * span;
+    nt = rem / a.R;
+    b = chunk_id * a.R + (rem - nt * a.R);
+    if (b >= nblocks) return;
+    if constexpr (ROUTED) {
+      e = a.expert_ids[b];
+      if (e >= a.E) return;
+    } else {
+      e = a.blk_expert[b];
+    }
+    if (e < 0) return;
   }
-  if (e < 0) return;
 
   if (tid == 0) s_rows = 0;
   __syncthreads();
@@ -791,6 +797,12 @@ static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
              (reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
   // output rows can be written in 16-byte pieces
   a.vec_out = (a.N % 8 == 0) && (a.ldo % 8 == 0) && (reinterpret_cast<uintptr_t>(a.out) % 16 == 0);
+  // Expert groups pay a short search per tile; they pay off when an expert's
+  // weights outgrow one XCD's 4 MB L2 (below that the weights stay cached
+  // across row blocks anyway). 128-row groups hold up to 4 blocks, 64-row
+  // groups 2 (set_grid has sized the grid for any grouping).
+  a.egroups = RMODE != 0 && BM >= 64 && !DEBUGP && (int64_t)a.N * (a.K / 2) > (int64_t)4 << 20;
+  if (a.egroups) a.R = BM >= 128 ? 4 : 2;
   if (a.total_tiles == 0) return hipSuccess;
   // the guard-free body needs whole chunks, a chunk count divisible by the
   // unroll, and (without the LDS zero/scale block) aligned vector runs

@@ -38,7 +38,38 @@ struct GemmArgs {
   int vec_out;                // output rows may be stored in 16-byte pieces (N, ldo multiples of 8; aligned)
   // launch geometry (see grid_for)
   int n_tiles, R, total_tiles, per_xcd;
+  int egroups;                // routed 64/128-row tiles in expert groups (expert_group_tile)
 };
+
+// Expert-grouped tile order of a routed launch. The row blocks of one
+// expert's run (expert_ids ascends over the blocks, as moe_align lays them
+// out) form groups of up to R blocks counted from the run's first block; a
+// group's tiles take the column tiles in turn, its blocks innermost, so the
+// tiles that share one column tile of one expert's weights are adjacent in
+// the list and run at the same time on one XCD. Every block keeps n_tiles
+// tiles inside its group's range, so block t / n_tiles lies in the group of
+// tile t. Writes block b, column tile nt and expert e of tile t in
+// [0, nblocks * n_tiles); false when the block has no expert in [0, E) or the
+// blocks are out of order.
+__host__ __device__ inline bool expert_group_tile(int t, int n_tiles, int R, int nblocks, const int32_t* expert_ids,
+                                                  int E, int& b, int& nt, int& e) {
+  const int bb = t / n_tiles;
+  e = expert_ids[bb];
+  if (e < 0 || e >= E) return false;
+  int lo = 0, hi = bb;   // first block of the run: lower bound of e in [0, bb]
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (expert_ids[mid] < e) lo = mid + 1;
+    else hi = mid;
+  }
+  const int g0 = lo + (bb - lo) / R * R;
+  int gs = 1;
+  while (gs < R && g0 + gs < nblocks && expert_ids[g0 + gs] == e) ++gs;
+  const int local = t - g0 * n_tiles;
+  nt = local / gs;
+  b = g0 + (local - nt * gs);
+  return nt < n_tiles;
+}
 
 struct TileConfig {
   int BM;     // rows per block
