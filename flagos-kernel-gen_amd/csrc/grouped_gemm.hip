@@ -46,6 +46,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr uint32_t kOOB = 0x80000000u;   // buffer offset that reads as zero
+// float bits of 12582912 = 1.5 * 2^23: adding an integer P with |P| <= 2^22 to
+// them gives the float 12582912 + P exactly
+constexpr int kMagic = 0x4B400000;
+constexpr float kMagicF = 12582912.0f;
 constexpr int kRsrcFlags = 0x00020000;   // raw buffer, 32-bit data format
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -362,10 +366,22 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[mb][nb][r] = 0.f;
+  const i32x4 magic4 = {kMagic, kMagic, kMagic, kMagic};
 
   // ---- one chunk of K ------------------------------------------------------
   // dd: position of the chunk in its zero/scale window (compile-time after unrolling)
+  //
+  // Fold without a convert: each group's MFMA chain starts from the integer
+  // kMagic = 0x4B400000 instead of 0, so the int32 result M + P (|P| <= 2^22
+  // for every group size here) read as a float is exactly 12582912 + P. One
+  // FMA then folds (12582912 + P) * s; the 12582912 * s of the chunk's groups
+  // is summed per column (bias) and subtracted from the accumulators once per
+  // chunk, which keeps their magnitude -- and the extra rounding -- small.
+  // (The debug-partials kernel keeps the plain int32 chain.)
   auto compute = [&](int ch, const int8_t* xb, const WChunk& wc, const ZsWin& zw, int dd) {
+    float bias[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) bias[nb] = 0.f;
 #pragma unroll
     for (int g = 0; g < KCG; ++g) {
       const int gg = ch * KCG + g;
@@ -405,13 +421,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
             sv[nb] *= 0.0625f;
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-              // repacked weights store every nibble with its top bit flipped
-              const uint32_t t0 = REPACKED ? wc.w[g][nb][2 * s] : wc.w[g][nb][2 * s] ^ 0x88888888u;
-              const uint32_t t1 = REPACKED ? wc.w[g][nb][2 * s + 1] : wc.w[g][nb][2 * s + 1] ^ 0x88888888u;
-              bfr[nb][s].x = (int)((t0 << 4) & 0xF0F0F0F0u);
-              bfr[nb][s].y = (int)(t0 & 0xF0F0F0F0u);
-              bfr[nb][s].z = (int)((t1 << 4) & 0xF0F0F0F0u);
-              bfr[nb][s].w = (int)(t1 & 0xF0F0F0F0u);
+              // the top-bit flip (repacked weights store it) is applied after
+              // the mask, so each half is a shift and one 3-input op
+              const uint32_t flip = REPACKED ? 0u : 0x80808080u;
+              const uint32_t t0 = wc.w[g][nb][2 * s];
+              const uint32_t t1 = wc.w[g][nb][2 * s + 1];
+              bfr[nb][s].x = (int)(((t0 << 4) & 0xF0F0F0F0u) ^ flip);
+              bfr[nb][s].y = (int)((t0 & 0xF0F0F0F0u) ^ flip);
+              bfr[nb][s].z = (int)(((t1 << 4) & 0xF0F0F0F0u) ^ flip);
+              bfr[nb][s].w = (int)((t1 & 0xF0F0F0F0u) ^ flip);
             }
           }
         } else {
@@ -429,6 +447,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
               bfr[nb][s].w = (int)fold_odd(d1, zf);
             }
           }
+        }
+        if constexpr (!DEBUGP) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) bias[nb] = __builtin_fmaf(kMagicF, sv[nb], bias[nb]);
         }
         // Software-pipelined over 16-row blocks: the A fragments of block
         // mb+1 are read from LDS while block mb's MFMAs run, and block mb-1's
@@ -456,7 +478,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
             for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
               for (int r = 0; r < 4; ++r)
-                acc[mb][nb][r] = __builtin_fmaf((float)part[nb][r], sv[nb], acc[mb][nb][r]);
+                acc[mb][nb][r] = __builtin_fmaf(__int_as_float(part[nb][r]), sv[nb], acc[mb][nb][r]);
           }
         };
         i32x4 av[2][S];
@@ -469,13 +491,21 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
           for (int s = 0; s < S; ++s)
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-              const i32x4 cin = (s == 0) ? i32x4{0, 0, 0, 0} : part[mb & 1][nb];
+              const i32x4 cin = (s == 0) ? (DEBUGP ? i32x4{0, 0, 0, 0} : magic4) : part[mb & 1][nb];
               part[mb & 1][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mb & 1][s], bfr[nb][s], cin, 0, 0, 0);
             }
           if (mb > 0) fold(mb - 1, part[(mb - 1) & 1]);
         }
         fold(MB - 1, part[(MB - 1) & 1]);
       }
+    }
+    if constexpr (!DEBUGP) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[mb][nb][r] -= bias[nb];
     }
   };
 
