@@ -289,7 +289,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   auto load_x = [&](int ch) {
 #pragma unroll
     for (int j = 0; j < XU; ++j)
-      xr[j] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, x_off[j] + (uint32_t)(ch * KC), 0, 0);
+      xr[j] = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, x_off[j], ch * KC, 0);
   };
   auto store_x = [&](int buf) {
 #pragma unroll
@@ -335,15 +335,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       const uint32_t gg = (uint32_t)(ch * KCG + g);
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const uint32_t off = w_off[nb] + gg * (GS / 2);
+        const uint32_t off = w_off[nb];
+        const int soff = (int)gg * (GS / 2);   // uniform part: the scalar offset
         if constexpr (S == 1) {
-          const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(w_rsrc, off, 0, 0);
+          const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(w_rsrc, off, soff, 0);
           d.w[g][nb][0] = q.x;
           d.w[g][nb][1] = q.y;
         } else {
 #pragma unroll
           for (int h = 0; h < S / 2; ++h) {
-            const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, off + 16 * h, 0, 0);
+            const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, off + 16 * h, soff, 0);
             d.w[g][nb][4 * h + 0] = q.x;
             d.w[g][nb][4 * h + 1] = q.y;
             d.w[g][nb][4 * h + 2] = q.z;
@@ -367,6 +368,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[mb][nb][r] = 0.f;
   const i32x4 magic4 = {kMagic, kMagic, kMagic, kMagic};
+  bool tile_sym = false;   // ZS_LDS: every zero point of the tile is 8
 
   // ---- one chunk of K ------------------------------------------------------
   // dd: position of the chunk in its zero/scale window (compile-time after unrolling)
@@ -374,14 +376,28 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // Fold without a convert: each group's MFMA chain starts from the integer
   // kMagic = 0x4B400000 instead of 0, so the int32 result M + P (|P| <= 2^22
   // for every group size here) read as a float is exactly 12582912 + P. One
-  // FMA then folds (12582912 + P) * s; the 12582912 * s of the chunk's groups
-  // is summed per column (bias) and subtracted from the accumulators once per
-  // chunk, which keeps their magnitude -- and the extra rounding -- small.
-  // (The debug-partials kernel keeps the plain int32 chain.)
-  auto compute = [&](int ch, const int8_t* xb, const WChunk& wc, const ZsWin& zw, int dd) {
-    float bias[NB];
+  // FMA then folds (12582912 + P) * s; the 12582912 * s of the groups is
+  // summed per column (bias) and subtracted from the accumulators (rebase)
+  // every RD chunks -- and right after any group whose zero points are not
+  // all 8, whose scales, and so bias, are 16x larger -- which keeps the
+  // accumulators' magnitude, and the extra rounding, small. (The
+  // debug-partials kernel keeps the plain int32 chain.)
+  float bias[NB];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) bias[nb] = 0.f;
+  for (int nb = 0; nb < NB; ++nb) bias[nb] = 0.f;
+  auto rebase = [&]() {
+    if constexpr (!DEBUGP) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[mb][nb][r] -= bias[nb];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) bias[nb] = 0.f;
+    }
+  };
+  auto compute = [&](int ch, const int8_t* xb, const WChunk& wc, const ZsWin& zw, int dd) {
 #pragma unroll
     for (int g = 0; g < KCG; ++g) {
       const int gg = ch * KCG + g;
@@ -402,14 +418,17 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
           }
         }
         i32x4 bfr[NB][S];
-        // Symmetric int4 (every zero point of this group in the wave is 8):
+        // Symmetric int4 (every zero point of the tile -- LDS block -- or of
+        // this group in the wave is 8):
         // 16 * (u - 8) is the nibble with its top bit flipped, moved into the
         // high half of its byte, so unpacking takes 2 ops per int8 dword
         // instead of 3.5. The partials come out 16x larger and the scale is
         // used / 16; both factors are powers of two and the product fed to
         // the FMA is the same real number, so the result is bit-identical.
         bool sym = false;
-        if constexpr (!DEBUGP) {
+        if constexpr (ZS_LDS && !DEBUGP) {
+          sym = tile_sym;   // scales already / 16
+        } else if constexpr (!DEBUGP) {
           bool z8 = true;
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) z8 = z8 && zv[nb] == 8;
@@ -418,7 +437,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         if (sym) {
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
-            sv[nb] *= 0.0625f;
+            if constexpr (!ZS_LDS) sv[nb] *= 0.0625f;
 #pragma unroll
             for (int s = 0; s < S; ++s) {
               // the top-bit flip (repacked weights store it) is applied after
@@ -497,15 +516,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
           if (mb > 0) fold(mb - 1, part[(mb - 1) & 1]);
         }
         fold(MB - 1, part[(MB - 1) & 1]);
+        // a group with other zero points has 16x larger scales (and bias):
+        // it is rebased at once, so the accumulators never hold more than one
+        // such group's bias
+        if (!sym) rebase();
       }
-    }
-    if constexpr (!DEBUGP) {
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[mb][nb][r] -= bias[nb];
     }
   };
 
@@ -535,11 +550,33 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     }
   }
   if constexpr (ZS_LDS) {
-    // visible to all waves after the first barrier of the loop
+    // visible to all waves after the first barrier of the loop. A tile whose
+    // zero points are all 8 (symmetric int4) is found here once, and its
+    // scales are stored / 16 for the symmetric unpack (see compute).
+    if constexpr (!DEBUGP) {
+      int ok = 1;
+#pragma unroll
+      for (int j = 0; j < ZU; ++j) {
+        const int u = tid + j * NT;
+        if (u < z_units)
+          ok &= (zq[j].x == 0x08080808u) & (zq[j].y == 0x08080808u) & (zq[j].z == 0x08080808u) &
+                (zq[j].w == 0x08080808u);
+      }
+      tile_sym = __syncthreads_and(ok) != 0;
+    }
 #pragma unroll
     for (int j = 0; j < SU; ++j) {
       const int u = tid + j * NT;
-      if (!DEBUGP && u < s_units) *reinterpret_cast<u32x4*>(s_scale + 4 * u) = sq[j];
+      if (!DEBUGP && u < s_units) {
+        u32x4 v = sq[j];
+        if (tile_sym) {
+          v.x = __float_as_uint(__uint_as_float(v.x) * 0.0625f);
+          v.y = __float_as_uint(__uint_as_float(v.y) * 0.0625f);
+          v.z = __float_as_uint(__uint_as_float(v.z) * 0.0625f);
+          v.w = __float_as_uint(__uint_as_float(v.w) * 0.0625f);
+        }
+        *reinterpret_cast<u32x4*>(s_scale + 4 * u) = v;
+      }
     }
 #pragma unroll
     for (int j = 0; j < ZU; ++j) {
@@ -590,6 +627,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       for (int ch = 0; ch < c.nchunks; ch += 2) {
         interval(ch, 0, std::true_type{});
         if (ch + 1 < c.nchunks) interval(ch + 1, 1, std::true_type{});
+        rebase();
       }
     } else {
       store_x(0);
@@ -597,6 +635,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       for (int ch = 0; ch < c.nchunks; ch += 2) {
         interval(ch, 0, std::false_type{});
         if (ch + 1 < c.nchunks) interval(ch + 1, 1, std::false_type{});
+        rebase();
       }
     }
   }
@@ -623,6 +662,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
       }
     }
+    rebase();
   }
 
   if constexpr (!DEBUGP) {
