@@ -974,11 +974,19 @@ TileConfig tiles_for_block_m(int BM, int group_size) {
 }
 
 TileConfig select_tiles(int rows, int touched_experts, int N, int K, int group_size) {
-  (void)N;
   const int ne = touched_experts < 1 ? 1 : touched_experts;
   const int per_expert = (rows + ne - 1) / ne;
-  if (per_expert <= 16) return tiles_for_block_m(16, group_size);
-  if (per_expert <= 32) return tiles_for_block_m(32, group_size);
+  // Measured on MI355X (DeepSeek-V3, Qwen3, Mixtral shapes): up to 8 rows per
+  // expert the 16-row decode tile streams the weights best; from 16 rows the
+  // 64-row tile wins (one block per expert reads its weights once, and its
+  // half-height body covers experts of up to 32 rows) -- by 16-40 % at 16-32
+  // rows; in between the long K = 7168 still prefers 16 rows, K <= 4096 64.
+  // The 32-row tile was never the fastest choice.
+  if (per_expert <= 8) return tiles_for_block_m(16, group_size);
+  if (per_expert < 16 && K > 4096) return tiles_for_block_m(16, group_size);
+  // a small problem keeps the 16-row tiles' larger grid (64-row tiles span
+  // 128 columns: fewer than 256 tiles leave CUs idle)
+  if (per_expert <= 32 && (int64_t)ne * ((N + 127) / 128) < 256) return tiles_for_block_m(16, group_size);
   // 128-row tiles pay off only over a long K loop (measured on MI355X:
   // K = 7168 prefers 128 rows, K = 2048 prefers 64)
   if (per_expert <= 64 || K < 4096) return tiles_for_block_m(64, group_size);

@@ -45,6 +45,15 @@ def test_sizes_and_tile_selection(pkg):
     assert pkg.select_block_m(32768, 256, 4096, 7168, 128) == 128
     assert pkg.select_block_m(512, 256, 4096, 7168, 128) == 16
     assert pkg.select_block_m(64 * 8, 8, 2048, 1024, 128) == 64
+    assert pkg.select_block_m(64 * 2, 8, 2048, 1024, 128) == 16         # tiny M=64: 16 rows, 128 tiles
+    # middle: 8 rows per expert stay on 16-row tiles; from 16 rows (and from
+    # 9 rows at K <= 4096) the 64-row tile (measured crossovers)
+    assert pkg.select_block_m(32 * 2, 8, 28672, 4096, 128) == 16        # Mixtral M=32: 8 rows
+    assert pkg.select_block_m(64 * 2, 8, 28672, 4096, 128) == 64        # Mixtral M=64: 16 rows
+    assert pkg.select_block_m(384 * 8, 256, 4096, 7168, 128) == 16     # DSv3 up M=384: 12 rows
+    assert pkg.select_block_m(384 * 8, 256, 7168, 2048, 128) == 64     # DSv3 down M=384: 12 rows
+    assert pkg.select_block_m(256 * 8, 128, 1536, 2048, 128) == 64     # Qwen3 M=256: 16 rows
+    assert pkg.select_block_m(1024 * 8, 256, 4096, 7168, 128) == 64    # DSv3 up M=1024: 32 rows
     # long expert row lists: 128-row tiles for a long K loop, 64 for a short one
     assert pkg.select_block_m(32768, 256, 7168, 2048, 128) == 64
     assert pkg.select_block_m(16384, 128, 1536, 2048, 128) == 64
