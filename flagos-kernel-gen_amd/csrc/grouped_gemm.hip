@@ -49,6 +49,15 @@ constexpr uint32_t kOOB = 0x80000000u;   // buffer offset that reads as zero
 // float bits of 12582912 = 1.5 * 2^23: adding an integer P with |P| <= 2^22 to
 // them gives the float 12582912 + P exactly
 constexpr int kMagic = 0x4B400000;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+// two fp32 -> packed bf16 (a low, b high), round to nearest even: one
+// v_cvt_pk_bf16_f32 (same bits as bf16_rne_bits for every non-NaN input)
+__device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
 constexpr float kMagicF = 12582912.0f;
 constexpr int kRsrcFlags = 0x00020000;   // raw buffer, 32-bit data format
 
@@ -686,13 +695,20 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
             const int cl = c.col0 - c.tile_col0 + nb * 16 + jl;
+            float v[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int row = mb * 16 + kb * 4 + r;
-              float v = acc[mb][nb][r] * s_xs[row];
-              if constexpr (ROUTED) v = v * s_tw[row];
+              v[r] = acc[mb][nb][r] * s_xs[row];
+              if constexpr (ROUTED) v[r] = v[r] * s_tw[row];
+            }
+            // rows r and r + 1 of the column converted as one pair
+            const uint32_t pk[2] = {bf16x2_rne(v[0], v[1]), bf16x2_rne(v[2], v[3])};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int row = mb * 16 + kb * 4 + r;
               const int off = row * ROWB + (((cl >> 3) ^ (row & (SEG - 1))) << 4) + ((cl & 7) << 1);
-              *reinterpret_cast<uint16_t*>(tile + off) = bf16_rne_bits(__float_as_uint(v));
+              *reinterpret_cast<uint16_t*>(tile + off) = (uint16_t)(pk[r >> 1] >> (16 * (r & 1)));
             }
           }
         __syncthreads();
