@@ -430,10 +430,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         // Symmetric int4 (every zero point of the tile -- LDS block -- or of
         // this group in the wave is 8):
         // 16 * (u - 8) is the nibble with its top bit flipped, moved into the
-        // high half of its byte, so unpacking takes 2 ops per int8 dword
+        // high half of its byte, so unpacking takes 1.5 ops per int8 dword
         // instead of 3.5. The partials come out 16x larger and the scale is
-        // used / 16; both factors are powers of two and the product fed to
-        // the FMA is the same real number, so the result is bit-identical.
+        // used / 16; both factors are powers of two, so the product fed to
+        // the fold is the same real number.
         bool sym = false;
         if constexpr (ZS_LDS && !DEBUGP) {
           sym = tile_sym;   // scales already / 16
