@@ -843,7 +843,15 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   c.col0 = nt * BN + wave * WN;
   c.nchunks = (a.G + KCG - 1) / KCG;
   c.rows = rows;
-  // tiles whose valid rows fit in the top half run the half-height body
+  // tiles whose valid rows fit in the top quarter (8-wave 128-row tiles: the
+  // second block of most DeepSeek-V3 experts) or half run a shorter body
+  if constexpr (BM >= 128 && NW == 8) {
+    if (rows <= BM / 4) {
+      gemm_body<BM / 4, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV>(a, c, s_x, s_scale, s_zero, s_src, s_dst,
+                                                                     s_xs, s_tw);
+      return;
+    }
+  }
   if constexpr (BM >= 64) {
     if (rows <= BM / 2) {
       gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV>(a, c, s_x, s_scale, s_zero, s_src, s_dst,
