@@ -131,8 +131,27 @@ def kernel_events(fn, n, warmup):
     return statistics.mean(ms) * 1e3, statistics.median(ms) * 1e3
 
 
+def prime(fn, min_ms=100.0):
+    """Untimed run of fn until ~min_ms of GPU work has completed, so that the
+    timed phases start with the GPU at its working clock (the first timed
+    phase after input generation otherwise measured ~5 % slow)."""
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    i = 0
+    while True:
+        fn(i)
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
+            if (time.perf_counter() - t0) * 1e3 >= min_ms:
+                break
+    torch.cuda.synchronize()
+
+
 def measure_point(pt, steps, warmup):
     import torch
+    prime(pt.step)
     us_step = time_steps(pt.step, steps, warmup) * 1e6
     us_gemm, us_gemm_med = kernel_events(pt.gemm, steps, warmup)
     n = pt.n_sets
@@ -193,6 +212,7 @@ class LayerPoint:
 def measure_layer(pkg, M, dev, steps, warmup):
     import torch
     lp = LayerPoint(pkg, M, dev)
+    prime(lp.layer)
     us = time_steps(lp.layer, steps, warmup) * 1e6
     out = {"workload": f"dsv3_layer:M={M}", "E": lp.E, "topk": lp.TOPK, "hidden": lp.H, "intermediate": lp.I,
            "us_per_layer": round(us, 2), "stages": []}
