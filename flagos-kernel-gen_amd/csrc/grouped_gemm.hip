@@ -206,7 +206,7 @@ struct TileCtx {
 //     join, and waited there for every outstanding load, which serialized
 //     the prefetch with the compute.
 template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST,
-          bool ZSV>
+          bool ZSV, bool SYMT>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, int8_t* s_x, float* s_scale,
                                           int8_t* s_zero, const int* s_src, const int* s_dst, const float* s_xs,
                                           const float* s_tw) {
@@ -224,6 +224,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   constexpr bool ZS_LDS = ZSG > 0;
   constexpr bool ROUTED = RMODE != 0;
   constexpr bool REPACKED = RMODE == kModeRoutedRepacked;
+  // SYMT: every zero point of the tile is 8 (decided by the kernel entry for
+  // tiles with an LDS zero/scale block): symmetric unpack and magic-number
+  // fold for every group, scales stored / 16, no zero points needed
+  constexpr bool MG = SYMT && ZS_LDS && !DEBUGP;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -285,7 +289,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 #pragma unroll
     for (int j = 0; j < ZU; ++j) {
       const int u = tid + j * NT;
-      if (u < z_units) zq[j] = __builtin_amdgcn_raw_buffer_load_b128(z_rsrc, zbase + u * 16u, 0, 0);
+      if (!MG && u < z_units) zq[j] = __builtin_amdgcn_raw_buffer_load_b128(z_rsrc, zbase + u * 16u, 0, 0);
     }
   }
   // LDS index of this lane's columns in the zero/scale block
@@ -377,7 +381,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[mb][nb][r] = 0.f;
   const i32x4 magic4 = {kMagic, kMagic, kMagic, kMagic};
-  bool tile_sym = false;   // ZS_LDS: every zero point of the tile is 8
 
   // ---- one chunk of K ------------------------------------------------------
   // dd: position of the chunk in its zero/scale window (compile-time after unrolling)
@@ -386,16 +389,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // kMagic = 0x4B400000 instead of 0, so the int32 result M + P (|P| <= 2^22
   // for every group size here) read as a float is exactly 12582912 + P. One
   // FMA then folds (12582912 + P) * s; the 12582912 * s of the groups is
-  // summed per column (bias) and subtracted from the accumulators (rebase)
-  // every RD chunks -- and right after any group whose zero points are not
-  // all 8, whose scales, and so bias, are 16x larger -- which keeps the
-  // accumulators' magnitude, and the extra rounding, small. (The
-  // debug-partials kernel keeps the plain int32 chain.)
+  // summed per column (bias) and subtracted from the accumulators every RD
+  // chunks (rebase), which keeps their magnitude, and the extra rounding,
+  // small. Only symmetric tiles with an LDS zero/scale block (SYMT: scales
+  // / 16, so a small bias) take this path; every other tile and kernel
+  // keeps the plain int32 chain and a convert.
   float bias[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) bias[nb] = 0.f;
   auto rebase = [&]() {
-    if constexpr (!DEBUGP) {
+    if constexpr (MG) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -435,8 +438,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         // used / 16; both factors are powers of two, so the product fed to
         // the fold is the same real number.
         bool sym = false;
-        if constexpr (ZS_LDS && !DEBUGP) {
-          sym = tile_sym;   // scales already / 16
+        if constexpr (MG) {
+          sym = true;   // scales already / 16
         } else if constexpr (!DEBUGP) {
           bool z8 = true;
 #pragma unroll
@@ -446,7 +449,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         if (sym) {
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
-            if constexpr (!ZS_LDS) sv[nb] *= 0.0625f;
+            if constexpr (!MG) sv[nb] *= 0.0625f;
 #pragma unroll
             for (int s = 0; s < S; ++s) {
               // the top-bit flip (repacked weights store it) is applied after
@@ -476,7 +479,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
             }
           }
         }
-        if constexpr (!DEBUGP) {
+        if constexpr (MG) {
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) bias[nb] = __builtin_fmaf(kMagicF, sv[nb], bias[nb]);
         }
@@ -505,8 +508,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-              for (int r = 0; r < 4; ++r)
-                acc[mb][nb][r] = __builtin_fmaf(__int_as_float(part[nb][r]), sv[nb], acc[mb][nb][r]);
+              for (int r = 0; r < 4; ++r) {
+                const float pf = MG ? __int_as_float(part[nb][r]) : (float)part[nb][r];
+                acc[mb][nb][r] = __builtin_fmaf(pf, sv[nb], acc[mb][nb][r]);
+              }
           }
         };
         i32x4 av[2][S];
@@ -519,16 +524,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
           for (int s = 0; s < S; ++s)
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-              const i32x4 cin = (s == 0) ? (DEBUGP ? i32x4{0, 0, 0, 0} : magic4) : part[mb & 1][nb];
+              const i32x4 cin = (s == 0) ? (MG ? magic4 : i32x4{0, 0, 0, 0}) : part[mb & 1][nb];
               part[mb & 1][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mb & 1][s], bfr[nb][s], cin, 0, 0, 0);
             }
           if (mb > 0) fold(mb - 1, part[(mb - 1) & 1]);
         }
         fold(MB - 1, part[(MB - 1) & 1]);
-        // a group with other zero points has 16x larger scales (and bias):
-        // it is rebased at once, so the accumulators never hold more than one
-        // such group's bias
-        if (!sym) rebase();
       }
     }
   };
@@ -559,26 +560,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     }
   }
   if constexpr (ZS_LDS) {
-    // visible to all waves after the first barrier of the loop. A tile whose
-    // zero points are all 8 (symmetric int4) is found here once, and its
-    // scales are stored / 16 for the symmetric unpack (see compute).
-    if constexpr (!DEBUGP) {
-      int ok = 1;
-#pragma unroll
-      for (int j = 0; j < ZU; ++j) {
-        const int u = tid + j * NT;
-        if (u < z_units)
-          ok &= (zq[j].x == 0x08080808u) & (zq[j].y == 0x08080808u) & (zq[j].z == 0x08080808u) &
-                (zq[j].w == 0x08080808u);
-      }
-      tile_sym = __syncthreads_and(ok) != 0;
-    }
+    // visible to all waves after the first barrier of the loop; a symmetric
+    // tile stores its scales / 16 for the symmetric unpack (see compute)
 #pragma unroll
     for (int j = 0; j < SU; ++j) {
       const int u = tid + j * NT;
       if (!DEBUGP && u < s_units) {
         u32x4 v = sq[j];
-        if (tile_sym) {
+        if constexpr (MG) {
           v.x = __float_as_uint(__uint_as_float(v.x) * 0.0625f);
           v.y = __float_as_uint(__uint_as_float(v.y) * 0.0625f);
           v.z = __float_as_uint(__uint_as_float(v.z) * 0.0625f);
@@ -590,7 +579,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 #pragma unroll
     for (int j = 0; j < ZU; ++j) {
       const int u = tid + j * NT;
-      if (u < z_units) *reinterpret_cast<u32x4*>(s_zero + 16 * u) = zq[j];
+      if (!MG && u < z_units) *reinterpret_cast<u32x4*>(s_zero + 16 * u) = zq[j];
     }
   }
   // STAGGER (8-wave 256-column tiles): half of the waves run the chunk
@@ -810,6 +799,25 @@ void w4a8_gemm_kernel(const GemmArgs a) {
 
   if (tid == 0) s_rows = 0;
   __syncthreads();
+  // Tiles with an LDS zero/scale block: is every zero point of the tile's
+  // [BN x G] block 8 (symmetric int4)? The loads go out with the routing
+  // rows' and are checked at the same barrier. Columns past N read zero
+  // (not symmetric).
+  constexpr bool SYM_CHECK = ZSG > 0 && !DEBUGP;
+  constexpr int ZCU = SYM_CHECK ? (BN * ZSG / 16 + NW * 64 - 1) / (NW * 64) : 1;
+  int zok = 1;
+  if constexpr (SYM_CHECK) {
+    const __amdgpu_buffer_rsrc_t zr = make_rsrc(a.wz + (int64_t)e * a.N * a.G, (uint32_t)(a.N * a.G));
+    const int z_units = BN * a.G / 16;
+#pragma unroll
+    for (int j = 0; j < ZCU; ++j) {
+      const int u = tid + j * NW * 64;
+      if (u < z_units) {
+        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(zr, (uint32_t)(nt * BN * a.G) + u * 16u, 0, 0);
+        zok &= (q.x == 0x08080808u) & (q.y == 0x08080808u) & (q.z == 0x08080808u) & (q.w == 0x08080808u);
+      }
+    }
+  }
   if (tid < BM) {
     int src = -1, dst = -1;
     float xsv = 0.f, twv = 1.f;
@@ -834,7 +842,7 @@ void w4a8_gemm_kernel(const GemmArgs a) {
     s_tw[tid] = twv;
     if (dst >= 0) atomicMax(&s_rows, tid + 1);
   }
-  __syncthreads();
+  const bool tsym = SYM_CHECK ? __syncthreads_and(zok) != 0 : (__syncthreads(), false);
   const int rows = __builtin_amdgcn_readfirstlane(s_rows);
 
   TileCtx c;
@@ -844,23 +852,33 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   c.nchunks = (a.G + KCG - 1) / KCG;
   c.rows = rows;
   // tiles whose valid rows fit in the top quarter (8-wave 128-row tiles: the
-  // second block of most DeepSeek-V3 experts) or half run a shorter body
-  if constexpr (BM >= 128 && NW == 8) {
-    if (rows <= BM / 4) {
-      gemm_body<BM / 4, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV>(a, c, s_x, s_scale, s_zero, s_src, s_dst,
-                                                                     s_xs, s_tw);
-      return;
+  // second block of most DeepSeek-V3 experts) or half run a shorter body;
+  // symmetric tiles run the magic-number fold (SYMT)
+  auto run = [&](auto symt_c) {
+    constexpr bool SYMT = decltype(symt_c)::value;
+    if constexpr (BM >= 128 && NW == 8) {
+      if (rows <= BM / 4) {
+        gemm_body<BM / 4, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero,
+                                                                                    s_src, s_dst, s_xs, s_tw);
+        return;
+      }
     }
-  }
-  if constexpr (BM >= 64) {
-    if (rows <= BM / 2) {
-      gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV>(a, c, s_x, s_scale, s_zero, s_src, s_dst,
-                                                                     s_xs, s_tw);
-      return;
+    if constexpr (BM >= 64) {
+      if (rows <= BM / 2) {
+        gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero,
+                                                                                    s_src, s_dst, s_xs, s_tw);
+        return;
+      }
     }
+    gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero, s_src,
+                                                                            s_dst, s_xs, s_tw);
+  };
+  if constexpr (SYM_CHECK) {
+    if (tsym) run(std::true_type{});
+    else run(std::false_type{});
+  } else {
+    run(std::false_type{});
   }
-  gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV>(a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs,
-                                                                        s_tw);
 }
 
 // ---------------------------------------------------------------------------

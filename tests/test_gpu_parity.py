@@ -240,6 +240,44 @@ def test_routed_tiny_full_compare(pkg, dev):
         assert_close(out, ref, 2048, f"tiny bm={bm}")
 
 
+@pytest.mark.parametrize("zero", ["symmetric", "uint4"])
+def test_routed_fold_precision(pkg, dev, zero):
+    """Long K (G = 56) through the 16-, 64- and 128-row tiles: every bf16
+    output lies within one bf16 ulp of the exact (float64) value plus 1e-4 of
+    the magnitude of its summed group terms. The fp32 fold keeps this with a
+    wide margin; a lost, doubled or late removal of the fold's bias would not
+    (its terms are ~1e4x the group products)."""
+    wl = pkg.workloads
+    shape = wl.MoEShape("prec", 4, 2, 7168, 256, (96,))
+    inp = wl.make_routed_inputs(shape, 96, zero=zero)
+    gs, topk, N = shape.group_size, shape.topk, shape.N
+    ids = inp.topk_ids.reshape(-1)
+    tw = inp.topk_weights.reshape(-1).double()
+    P = ids.numel()
+    exact = torch.zeros(P, N, dtype=torch.float64)
+    mag = torch.zeros(P, N, dtype=torch.float64)
+    for e in range(shape.E):
+        sel = (ids == e).nonzero().reshape(-1)
+        if sel.numel() == 0:
+            continue
+        tok = sel // topk
+        w_e = task1_ref.fold_zero(task1_ref.unpack_int4(inp.w_q4[e]), inp.w_zero[e], gs)
+        terms = task1_ref.group_partials(inp.x_q[tok], w_e, gs).double() * inp.w_scale[e].double().unsqueeze(0)
+        rs = (inp.x_scale[tok].double() * tw[sel]).unsqueeze(-1)
+        exact[sel] = terms.sum(-1) * rs
+        mag[sel] = terms.abs().sum(-1) * rs.abs()
+    _, ex = np.frexp(exact.abs().numpy())
+    ulp = torch.from_numpy(np.ldexp(1.0, ex - 8))    # bf16 spacing at |exact|
+    args = [t.to(dev) for t in (inp.x_q, inp.x_scale, inp.w_q4, inp.w_scale, inp.w_zero, inp.topk_ids,
+                                inp.topk_weights)]
+    for bm in (16, 64, 128):
+        out = pkg.w4a8_fused_moe(*args, group_size=gs, block_m=bm).cpu().double()
+        err = (out - exact).abs()
+        bad = err > ulp + 1e-4 * mag
+        assert not bad.any(), (f"{zero} bm={bm}: {int(bad.sum())} outputs off by more than 1 ulp + 1e-4*|terms| "
+                               f"(worst {float((err - ulp - 1e-4 * mag).max()):.3g})")
+
+
 def test_routed_unrouted_pairs_untouched(pkg, dev):
     wl = pkg.workloads
     inp = wl.make_routed_inputs(wl.CONFIGS["tiny"], 16)
