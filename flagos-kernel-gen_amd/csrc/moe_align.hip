@@ -26,6 +26,17 @@
 //   workgroup. Padding slots, expert_ids and the tails are split over the
 //   workgroups by expert and by slot. No workgroup depends on another.
 //
+// moe_align_small_kernel: the same result for at most 64 pairs (decode),
+//   with no loop over experts. The first wave holds one pair per lane and
+//   takes one ballot per id bit. From those ballots alone (read from the
+//   top bit down) a lane gets the pairs of lower experts below it, and an
+//   expert's padded block count is the number of its pairs whose rank is a
+//   multiple of BM, so the same count over those "block heads" gives every
+//   expert's first block. Pairs are stored at once; each head records its
+//   block's expert and pair count in LDS. All four waves then write the
+//   padding, expert_ids, expert_offsets (the same counts per expert from
+//   the ballots, kept in LDS) and the tails (16-byte stores).
+//
 // csr_block_table_kernel: CSR expert_offsets (reference layout,
 //   docs/Task1.md:87-92) -> list of (expert, first row, end row) blocks of
 //   at most BM rows, so the GEMM grid needs no host-side count.
@@ -296,13 +307,113 @@ int align_workgroups(int num_pairs) {
   return nb < 64 ? nb : 64;
 }
 
+constexpr int kSmallPairs = 64;     // one pair per lane of the first wave
+constexpr int kSmallThreads = 256;
+constexpr int kIdBits = 10;         // ids below kAlignMaxE = 1024
+
+// pairs among `pm` whose id is below v (v < 1024), from the ballots of each
+// id bit: at every bit where v has a 1, the lanes still matching v's higher
+// bits and holding a 0 there are below v
+__device__ inline int count_below(int v, uint64_t pm, const uint64_t (&m)[kIdBits]) {
+  int n = 0;
+#pragma unroll
+  for (int bit = kIdBits - 1; bit >= 0; --bit) {
+    if ((v >> bit) & 1) {
+      n += __popcll(pm & ~m[bit]);
+      pm &= m[bit];
+    } else {
+      pm &= ~m[bit];
+    }
+  }
+  return n;
+}
+
+__global__ __launch_bounds__(kSmallThreads) void moe_align_small_kernel(
+    const int32_t* __restrict__ topk_ids, int P, int E, int BM,
+    int32_t* __restrict__ sorted_ids, int sorted_len,
+    int32_t* __restrict__ expert_ids, int blocks_len,
+    int32_t* __restrict__ num_post_pad, int32_t* __restrict__ expert_offsets) {
+  __shared__ uint64_t s_mask[kIdBits + 1];   // ballot of each id bit, then the routed pairs
+  __shared__ int s_bexp[kSmallPairs];        // expert of each padded block (>= 1 pair each)
+  __shared__ int s_bfill[kSmallPairs];       // pairs in each padded block
+  __shared__ int s_totblk;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  if (wave == 0) {
+    const int ev = lane < P ? topk_ids[lane] : -1;
+    const bool valid = (unsigned)ev < (unsigned)E;
+    const uint64_t vmask = __ballot(valid);
+    // the lanes holding the same expert; a lane's rank among them is its
+    // pair order within the expert (ids >= E and < 0 are not routed)
+    uint64_t m[kIdBits];
+    uint64_t peers = vmask;
+#pragma unroll
+    for (int bit = 0; bit < kIdBits; ++bit) {
+      const bool set = (ev >> bit) & 1;
+      m[bit] = __ballot(set);
+      peers &= set ? m[bit] : ~m[bit];
+    }
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const int rank = __popcll(peers & lt_mask);
+    const int c = __popcll(peers);
+    // an expert's padded blocks = its pairs whose rank is a multiple of BM
+    const bool head = valid && rank % BM == 0;
+    const uint64_t heads = __ballot(head);
+    const int bbelow = count_below(ev, vmask & heads, m);
+    if (valid) sorted_ids[bbelow * BM + rank] = lane;
+    if (head) {
+      const int b = bbelow + rank / BM;
+      s_bexp[b] = ev;
+      s_bfill[b] = min(BM, c - rank);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int bit = 0; bit < kIdBits; ++bit) s_mask[bit] = m[bit];
+      s_mask[kIdBits] = vmask;
+      s_totblk = __popcll(heads);
+      num_post_pad[0] = __popcll(heads) * BM;
+    }
+  }
+  __syncthreads();
+  const int tot_blk = s_totblk;
+  // padding slots: wave w takes blocks w, w + 4, ...; lane l holds block l's pairs
+  const int fill = lane < tot_blk ? s_bfill[lane] : 0;
+  for (int b = wave; b < tot_blk; b += kSmallThreads / 64) {
+    const int fb = __builtin_amdgcn_readlane(fill, b);
+    for (int q = fb + lane; q < BM; q += 64) sorted_ids[b * BM + q] = P;
+  }
+  for (int b = tid; b < blocks_len; b += kSmallThreads) expert_ids[b] = b < tot_blk ? s_bexp[b] : -1;
+  if (expert_offsets) {
+    uint64_t m[kIdBits];
+#pragma unroll
+    for (int bit = 0; bit < kIdBits; ++bit) m[bit] = s_mask[bit];
+    const uint64_t vmask = s_mask[kIdBits];
+    for (int e = tid; e <= E; e += kSmallThreads)
+      expert_offsets[e] = e < E ? count_below(e, vmask, m) : __popcll(vmask);
+  }
+  // tail: 16-byte stores from the first aligned slot on
+  const int t0 = tot_blk * BM;
+  const int mis = (int)((reinterpret_cast<uintptr_t>(sorted_ids + t0) >> 2) & 3);
+  const int hd = min(sorted_len, t0 + ((4 - mis) & 3));
+  if (tid < hd - t0) sorted_ids[t0 + tid] = P;
+  const int nv = (sorted_len - hd) >> 2;
+  int4* vt = reinterpret_cast<int4*>(sorted_ids + hd);
+  for (int i = tid; i < nv; i += kSmallThreads) vt[i] = make_int4(P, P, P, P);
+  const int rest = hd + nv * 4;
+  if (tid < sorted_len - rest) sorted_ids[rest + tid] = P;
+}
+
 hipError_t launch_moe_align(const int32_t* topk_ids, int num_pairs, int E, int BM,
                             int32_t* sorted_ids, int sorted_len, int32_t* expert_ids, int blocks_len,
                             int32_t* num_post_pad, int32_t* expert_offsets, hipStream_t s) {
   int id_bits = 0;
   while ((1 << id_bits) < E) ++id_bits;
   const int nb = align_workgroups(num_pairs);
-  if (nb > 1)
+  if (num_pairs <= kSmallPairs)
+    hipLaunchKernelGGL(moe_align_small_kernel, dim3(1), dim3(kSmallThreads), 0, s, topk_ids, num_pairs, E, BM,
+                       sorted_ids, sorted_len, expert_ids, blocks_len, num_post_pad, expert_offsets);
+  else if (nb > 1)
     hipLaunchKernelGGL(moe_align_split_kernel, dim3(nb), dim3(kAlignThreads), 0, s, topk_ids, num_pairs, E, BM,
                        id_bits, sorted_ids, sorted_len, expert_ids, blocks_len, num_post_pad, expert_offsets);
   else

@@ -42,6 +42,15 @@ ALIGN_CASES = [
     (64, 8, 2, 64, "softmax"),
     (3000, 1024, 4, 32, "uniform"),
     (5, 1, 1, 16, "softmax"),
+    # up to 64 pairs: the one-workgroup ballot kernel
+    (8, 1024, 8, 16, "uniform"),
+    (7, 128, 8, 64, "uniform"),
+    (2, 8, 2, 1, "softmax"),
+    (64, 4, 1, 128, "uniform"),
+    (9, 256, 7, 32, "softmax"),
+    (64, 64, 1, 1, "uniform"),
+    (16, 1024, 4, 3, "uniform"),
+    (8, 33, 8, 5, "softmax"),
 ]
 
 
@@ -55,6 +64,21 @@ def test_align_bit_exact(pkg, dev, M, E, topk, BM, kind):
     assert np.array_equal(x.cpu().numpy(), rx)
     assert int(n.item()) == int(rn)
     assert np.array_equal(o.cpu().numpy(), ro)
+
+
+def test_align_small_out_of_range_ids(pkg, dev):
+    """64 pairs with ids below 0, at E and far above it (bits past the id
+    width), mixed with repeated valid ids."""
+    g = torch.Generator().manual_seed(7)
+    ids = torch.randint(0, 40, (16, 4), generator=g, dtype=torch.int32)
+    ids[::3, 1] = 40
+    ids[1::5, 2] = -3
+    ids[2::4, 3] = 40 + 1024 * 3 + 5
+    for E, BM in ((40, 16), (40, 1), (1024, 7)):
+        s, x, n, o = pkg.moe_align_block_size(ids.to(dev), BM, E)
+        rs, rx, rn, ro = routing.moe_align_ref(ids.numpy(), E, BM)
+        assert np.array_equal(s.cpu().numpy(), rs) and np.array_equal(x.cpu().numpy(), rx)
+        assert int(n.item()) == int(rn) and np.array_equal(o.cpu().numpy(), ro)
 
 
 def test_align_out_of_range_ids_and_empty(pkg, dev):
