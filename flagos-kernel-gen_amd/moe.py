@@ -47,6 +47,24 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
+_ROUTING: dict = {}
+
+
+def _routing_buffer(device: torch.device, stream: int, n_int32: int) -> torch.Tensor:
+    """Per-(device, stream) int32 buffer for the routing metadata of
+    ``w4a8_fused_moe`` calls without precomputed routing, grown on demand.
+
+    A call's routing kernel writes it and the call's GEMM reads it; a later
+    call on the same stream runs after both, so the calls may share it.
+    """
+    key = (device.index, stream)
+    buf = _ROUTING.get(key)
+    if buf is None or buf.numel() < n_int32:
+        buf = torch.empty(max(n_int32, 1024), dtype=torch.int32, device=device)
+        _ROUTING[key] = buf
+    return buf
+
+
 def _need(cond: bool, msg: str, exc=W4A8ShapeError):
     if not cond:
         raise exc(msg)
@@ -225,20 +243,29 @@ def w4a8_fused_moe(x_q: torch.Tensor, x_scale: torch.Tensor, w_q4_packed: torch.
         return out
     if block_m is None:
         block_m = select_block_m(P, E, N, K, group_size)
-    if routing is None:
-        routing = moe_align_block_size(topk_ids.contiguous(), block_m, E)
-    else:
+    if routing is not None:
         sl, bl = align_buffer_sizes(P, E, block_m)
         _need(routing[0].numel() == sl and routing[1].numel() == bl,
               f"routing buffers do not match block_m={block_m} (expected lengths {sl} and {bl})")
         _on_gpu(dict(sorted_ids=routing[0], expert_ids=routing[1], num_tokens_post_padded=routing[2]))
-    sorted_ids, expert_ids, num_post = routing[0], routing[1], routing[2]
-    entry = _lib.lib().mw4a8_fused_moe if weight_layout == "reference" else _lib.lib().mw4a8_fused_moe_repacked
+    L = _lib.lib()
+    stream = ctypes.c_void_p(_stream(dev))
+    if routing is None:
+        # internal routing metadata: carved from the stream's cached int32
+        # buffer (no allocation per call)
+        sl, bl = align_buffer_sizes(P, E, block_m)
+        base = _routing_buffer(dev, stream.value, sl + bl + 1).data_ptr()
+        sorted_p, expert_p, num_post_p = base, base + 4 * sl, base + 4 * (sl + bl)
+        ids = topk_ids if topk_ids.is_contiguous() else topk_ids.contiguous()
+        _lib.check(L.mw4a8_moe_align(_ptr(ids), P, E, block_m, sorted_p, expert_p, num_post_p, None, stream),
+                   "mw4a8_moe_align")
+    else:
+        sorted_p, expert_p, num_post_p = routing[0].data_ptr(), routing[1].data_ptr(), routing[2].data_ptr()
+    entry = L.mw4a8_fused_moe if weight_layout == "reference" else L.mw4a8_fused_moe_repacked
     rc = entry(_ptr(x_q), x_q.stride(0), _ptr(x_scale), _ptr(w_q4_packed), _ptr(w_scale),
-                                    _ptr(w_zero), _ptr(sorted_ids), _ptr(expert_ids), _ptr(num_post),
-                                    _ptr(topk_weights) if topk_weights is not None else None, topk, _ptr(out),
-                                    out.stride(0), M, N, K, E, group_size,
-                                    block_m, ctypes.c_void_p(_stream(dev)))
+               _ptr(w_zero), sorted_p, expert_p, num_post_p,
+               _ptr(topk_weights) if topk_weights is not None else None, topk, _ptr(out),
+               out.stride(0), M, N, K, E, group_size, block_m, stream)
     _lib.check(rc, "mw4a8_fused_moe")
     return out
 

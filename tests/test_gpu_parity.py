@@ -319,6 +319,36 @@ def test_routed_unrouted_pairs_untouched(pkg, dev):
     assert_close(out, ref, 2048, "unrouted")
 
 
+def test_routed_shared_routing_buffer(pkg, dev):
+    """Calls without precomputed routing share one routing buffer per stream:
+    back-to-back calls of different sizes (the buffer shrinks in use and then
+    grows), a call on a second stream and a non-contiguous topk_ids view all
+    match the oracle."""
+    wl = pkg.workloads
+    cases = []
+    for M in (48, 5, 200):
+        inp = wl.make_routed_inputs(wl.CONFIGS["tiny"], M)
+        ref = task1_ref.fused_moe_ref(inp.x_q, inp.x_scale, inp.w_q4, inp.w_scale, inp.w_zero, inp.topk_ids,
+                                      inp.topk_weights, 128)
+        g = [t.to(dev) for t in (inp.x_q, inp.x_scale, inp.w_q4, inp.w_scale, inp.w_zero, inp.topk_ids,
+                                 inp.topk_weights)]
+        cases.append((M, g, ref))
+    outs = [pkg.w4a8_fused_moe(*g, group_size=128) for _, g, _ in cases]   # no sync in between
+    for (M, _, ref), out in zip(cases, outs):
+        assert_close(out.cpu(), ref, 2048, f"shared buffer M={M}")
+    M, g, ref = cases[0]
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        out = pkg.w4a8_fused_moe(*g, group_size=128)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    assert_close(out.cpu(), ref, 2048, "side stream")
+    ids_t = g[5].t().contiguous().t()    # same values, column-major
+    assert not ids_t.is_contiguous()
+    out = pkg.w4a8_fused_moe(*g[:5], ids_t, g[6], group_size=128)
+    assert_close(out.cpu(), ref, 2048, "non-contiguous topk_ids")
+
+
 POINTS = [("mixtral_up", 1), ("mixtral_up", 8), ("mixtral_up", 32),
           ("qwen3_up", 16), ("qwen3_up", 256), ("qwen3_up", 2048),
           ("dsv3_up", 1), ("dsv3_up", 64), ("dsv3_up", 4096),
