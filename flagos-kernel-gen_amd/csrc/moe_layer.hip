@@ -57,15 +57,28 @@ __device__ __forceinline__ float block_max(float v, float* s_red) {
 }
 
 // Per-token symmetric int8: scale = max(amax, 1e-12) / 127,
-// q = clamp(round_half_even(v / scale), -127, 127). IEEE division and
-// rint() make it bit-identical to the same float32 steps on the CPU.
+// q = clamp(round_half_even(v / scale), -127, 127), bit-identical to the
+// same float32 steps on the CPU (IEEE scale division; rint_div below).
 __device__ __forceinline__ float row_scale(float amax) { return fmaxf(amax, 1e-12f) / 127.0f; }
 
-__device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, float scale) {
-  const int qa = (int)fminf(fmaxf(rintf(a / scale), -127.f), 127.f);
-  const int qb = (int)fminf(fmaxf(rintf(b / scale), -127.f), 127.f);
-  const int qc = (int)fminf(fmaxf(rintf(c / scale), -127.f), 127.f);
-  const int qd = (int)fminf(fmaxf(rintf(d / scale), -127.f), 127.f);
+// rintf(a / s) for |a / s| <= 128 without dividing in the common case, and
+// bit-identical to it: t = a * inv (inv = 1 / s rounded) is within 2e-5 of
+// the rounded quotient (two roundings of relative size 2^-24 at |t| <= 128,
+// plus the quotient's own half ulp), and t - floor(t) is exact, so when t is
+// at least 1e-4 from a half-integer both round to the same integer. Lanes
+// closer than that (about 2 in 10^4) take the IEEE division. NaN and inf
+// inputs fail the test and give what the division gives.
+__device__ __forceinline__ float rint_div(float a, float s, float inv) {
+  const float t = a * inv;
+  if (fabsf((t - floorf(t)) - 0.5f) < 1e-4f) return rintf(a / s);
+  return rintf(t);
+}
+
+__device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, float scale, float inv) {
+  const int qa = (int)fminf(fmaxf(rint_div(a, scale, inv), -127.f), 127.f);
+  const int qb = (int)fminf(fmaxf(rint_div(b, scale, inv), -127.f), 127.f);
+  const int qc = (int)fminf(fmaxf(rint_div(c, scale, inv), -127.f), 127.f);
+  const int qd = (int)fminf(fmaxf(rint_div(d, scale, inv), -127.f), 127.f);
   return (uint32_t)(qa & 0xff) | ((uint32_t)(qb & 0xff) << 8) | ((uint32_t)(qc & 0xff) << 16) |
          ((uint32_t)(qd & 0xff) << 24);
 }
@@ -95,6 +108,7 @@ __global__ __launch_bounds__(kRowThreads) void quant_rows_kernel(const uint16_t*
       for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
     }
     const float s = row_scale(block_max(amax, s_red));
+    const float inv = 1.0f / s;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int c = (threadIdx.x + j * kRowThreads) * 8;
@@ -102,8 +116,8 @@ __global__ __launch_bounds__(kRowThreads) void quant_rows_kernel(const uint16_t*
         float f[8];
         unpack8(v[j], f);
         u32x2 o;
-        o.x = quant4(f[0], f[1], f[2], f[3], s);
-        o.y = quant4(f[4], f[5], f[6], f[7], s);
+        o.x = quant4(f[0], f[1], f[2], f[3], s, inv);
+        o.y = quant4(f[4], f[5], f[6], f[7], s, inv);
         *reinterpret_cast<u32x2*>(qr + c) = o;
       }
     }
@@ -116,12 +130,13 @@ __global__ __launch_bounds__(kRowThreads) void quant_rows_kernel(const uint16_t*
       for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
     }
     const float s = row_scale(block_max(amax, s_red));
+    const float inv = 1.0f / s;
     for (int c = threadIdx.x * 8; c < K; c += kRowThreads * 8) {
       float f[8];
       unpack8(*reinterpret_cast<const u32x4*>(xr + c), f);
       u32x2 o;
-      o.x = quant4(f[0], f[1], f[2], f[3], s);
-      o.y = quant4(f[4], f[5], f[6], f[7], s);
+      o.x = quant4(f[0], f[1], f[2], f[3], s, inv);
+      o.y = quant4(f[4], f[5], f[6], f[7], s, inv);
       *reinterpret_cast<u32x2*>(qr + c) = o;
     }
     if (threadIdx.x == 0) scale[row] = s;
@@ -131,7 +146,12 @@ __global__ __launch_bounds__(kRowThreads) void quant_rows_kernel(const uint16_t*
 // y = silu(gate) * up in fp32 as sigmoid = 1 / (1 + exp(-g)), silu = g *
 // sigmoid, y = silu * up (reference docs/Task3.md:103-110 order).
 __device__ __forceinline__ float silu_mul(float g, float u) {
-  const float sg = 1.0f / (1.0f + expf(-g));
+  // 1 / d as the hardware reciprocal plus one Newton step (within an ulp of
+  // the IEEE quotient); d = inf (exp overflow) gives 0 as the division does
+  const float d = 1.0f + expf(-g);
+  float sg = __builtin_amdgcn_rcpf(d);
+  sg = __builtin_fmaf(__builtin_fmaf(-d, sg, 1.0f), sg, sg);
+  if (__builtin_isinf(d)) sg = 0.0f;
   return (g * sg) * u;
 }
 
@@ -163,14 +183,15 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_quant_kernel(const uint1
       }
     }
     const float s = row_scale(block_max(amax, s_red));
+    const float inv = 1.0f / s;
     int8_t* qr = q + row * ldq;
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int c = (threadIdx.x + j * kRowThreads) * 8;
       if (c < I) {
         u32x2 o;
-        o.x = quant4(y[j][0], y[j][1], y[j][2], y[j][3], s);
-        o.y = quant4(y[j][4], y[j][5], y[j][6], y[j][7], s);
+        o.x = quant4(y[j][0], y[j][1], y[j][2], y[j][3], s, inv);
+        o.y = quant4(y[j][4], y[j][5], y[j][6], y[j][7], s, inv);
         *reinterpret_cast<u32x2*>(qr + c) = o;
       }
     }
@@ -185,6 +206,7 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_quant_kernel(const uint1
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(silu_mul(g[i], u[i])));
   }
   const float s = row_scale(block_max(amax, s_red));
+    const float inv = 1.0f / s;
   int8_t* qr = q + row * ldq;
   for (int c = threadIdx.x * 8; c < I; c += kRowThreads * 8) {
     float g[8], u[8], y[8];
@@ -193,8 +215,8 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_quant_kernel(const uint1
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = silu_mul(g[i], u[i]);
     u32x2 o;
-    o.x = quant4(y[0], y[1], y[2], y[3], s);
-    o.y = quant4(y[4], y[5], y[6], y[7], s);
+    o.x = quant4(y[0], y[1], y[2], y[3], s, inv);
+    o.y = quant4(y[4], y[5], y[6], y[7], s, inv);
     *reinterpret_cast<u32x2*>(qr + c) = o;
   }
   if (threadIdx.x == 0) scale[row] = s;

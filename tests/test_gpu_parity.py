@@ -349,6 +349,30 @@ def test_routed_shared_routing_buffer(pkg, dev):
     assert_close(out.cpu(), ref, 2048, "non-contiguous topk_ids")
 
 
+@pytest.mark.parametrize("zero", ["symmetric", "uint4"])
+def test_routed_short_last_blocks(pkg, dev, zero):
+    """128-row tiles at K = 7168 with experts whose last block is short:
+    loads 129, 144, 145, 128, 0, 300, 1 and 16 (last blocks of 1, 16, 17,
+    128, 44, 1 and 16 rows: quarter-, half- and full-height bodies, empty
+    experts); every pair row must be written, with the oracle's value."""
+    wl = pkg.workloads
+    loads = [129, 144, 145, 128, 0, 300, 1, 16]
+    E, K, N, gs = len(loads), 7168, 256, 128
+    M = sum(loads)
+    g = torch.Generator().manual_seed(41)
+    labels = torch.cat([torch.full((c,), e, dtype=torch.int32) for e, c in enumerate(loads)])
+    ids = labels[torch.randperm(M, generator=g)].reshape(M, 1).contiguous()
+    tw = torch.rand(M, 1, generator=g) + 0.5
+    w_q4, w_scale, w_zero = wl.make_weights(E, N, K, gs, 43, "cpu", zero)
+    x_q, x_scale = wl.make_activations(M, K, 44, "cpu")
+    out0 = torch.full((M, N), 7.0, dtype=torch.bfloat16)
+    ref = task1_ref.fused_moe_ref(x_q, x_scale, w_q4, w_scale, w_zero, ids, tw, gs, out=out0.clone())
+    out = out0.to(dev)
+    pkg.w4a8_fused_moe(*[t.to(dev) for t in (x_q, x_scale, w_q4, w_scale, w_zero, ids, tw)], group_size=gs,
+                       out=out, block_m=128)
+    assert_close(out, ref, N, f"short last blocks {zero}")
+
+
 POINTS = [("mixtral_up", 1), ("mixtral_up", 8), ("mixtral_up", 32),
           ("qwen3_up", 16), ("qwen3_up", 256), ("qwen3_up", 2048),
           ("dsv3_up", 1), ("dsv3_up", 64), ("dsv3_up", 4096),

@@ -45,6 +45,31 @@ def test_quant_matches_python_brute_force():
             assert int(q[m, k]) == want
 
 
+def test_reciprocal_rounding_with_division_fallback_equals_division():
+    """The quant kernels round a * (1/s) and divide only when that product is
+    within 1e-4 of a half-integer; for |a| <= 127 s this gives rint(a / s)
+    exactly (float32, round half to even). Half of the samples sit within 4
+    ulps of a half-integer multiple of s, where a plain a * (1/s) does differ
+    from the quotient."""
+    rng = np.random.default_rng(7)
+    n = 2_000_000
+    amax = (0.5 + rng.random(n, dtype=np.float32)) * np.exp2(rng.integers(-30, 30, n)).astype(np.float32)
+    s = np.maximum(amax, np.float32(1e-12)) / np.float32(127)
+    inv = np.float32(1) / s
+    a = ((rng.random(n, dtype=np.float32) * 2 - 1) * amax).astype(np.float32)
+    half = n // 2
+    k = (rng.integers(-127, 127, half) + 0.5).astype(np.float32)
+    near = (k * s[:half]).view(np.int32) + rng.integers(-4, 5, half).astype(np.int32)
+    a[:half] = near.view(np.float32)
+    keep = np.abs(a) <= amax
+    a, s, inv = a[keep], s[keep], inv[keep]
+    exact = np.rint(a / s)
+    t = a * inv
+    fast = np.where(np.abs((t - np.floor(t)) - np.float32(0.5)) < np.float32(1e-4), np.rint(a / s), np.rint(t))
+    assert np.array_equal(fast, exact)
+    assert not np.array_equal(np.rint(t), exact)   # the fallback is needed
+
+
 def test_quant_matches_the_benchmark_generator(pkg):
     g = torch.Generator().manual_seed(9)
     x = torch.randn(7, 96, generator=g).to(torch.bfloat16)
