@@ -145,13 +145,12 @@ __global__ __launch_bounds__(kRowThreads) void quant_rows_kernel(const uint16_t*
 
 // y = silu(gate) * up in fp32 as sigmoid = 1 / (1 + exp(-g)), silu = g *
 // sigmoid, y = silu * up (reference docs/Task3.md:103-110 order).
+// exp and the reciprocal are the hardware's (v_exp_f32 of -g * log2(e),
+// v_rcp_f32): about 1e-6 relative for |g| <= 16, against the ~10 VALU ops
+// of a correctly rounded expf that made this kernel ALU-bound; exp overflow
+// gives rcp(inf) = 0, as the division does.
 __device__ __forceinline__ float silu_mul(float g, float u) {
-  // 1 / d as the hardware reciprocal plus one Newton step (within an ulp of
-  // the IEEE quotient); d = inf (exp overflow) gives 0 as the division does
-  const float d = 1.0f + expf(-g);
-  float sg = __builtin_amdgcn_rcpf(d);
-  sg = __builtin_fmaf(__builtin_fmaf(-d, sg, 1.0f), sg, sg);
-  if (__builtin_isinf(d)) sg = 0.0f;
+  const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
   return (g * sg) * u;
 }
 
@@ -390,6 +389,61 @@ __global__ __launch_bounds__(256) void repack_weights_kernel(const uint32_t* __r
   if (t < n_words) dst[t] = inverse ? to_reference_order(src[t]) : to_mfma_order(src[t]);
 }
 
+// SiLU requant with a row per wave (kWaveRows rows per workgroup), for rows
+// of at most 4 eight-element chunks per lane: lane l holds chunks j at
+// elements 8 * (64 j + l), so each load instruction reads 1 KB of contiguous
+// row and all of a lane's loads are in flight before the row max, which is
+// a wave reduction (no LDS, no barrier). Same arithmetic as
+// silu_mul_quant_kernel, so the same bits. (For quant_rows the workgroup
+// kernel measured faster.)
+constexpr int kWaveRows = 4;
+
+template <int CH>
+__global__ __launch_bounds__(64 * kWaveRows) void silu_mul_quant_wave_kernel(const uint16_t* __restrict__ h,
+                                                                             int64_t ldh, int P, int I,
+                                                                             int8_t* __restrict__ q, int64_t ldq,
+                                                                             float* __restrict__ scale) {
+  const int64_t row = (int64_t)blockIdx.x * kWaveRows + (threadIdx.x >> 6);
+  if (row >= P) return;
+  const int lane = threadIdx.x & 63;
+  const uint16_t* hr = h + row * ldh;
+  u32x4 gv[CH], uv[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = (j * 64 + lane) * 8;
+    const bool ok = c < I;
+    gv[j] = ok ? *reinterpret_cast<const u32x4*>(hr + c) : u32x4{0, 0, 0, 0};
+    uv[j] = ok ? *reinterpret_cast<const u32x4*>(hr + I + c) : u32x4{0, 0, 0, 0};
+  }
+  float y[CH][8];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    float g[8], u[8];
+    unpack8(gv[j], g);
+    unpack8(uv[j], u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      y[j][i] = silu_mul(g[i], u[i]);
+      amax = fmaxf(amax, fabsf(y[j][i]));
+    }
+  }
+  const float s = row_scale(wave_max(amax));
+  const float inv = 1.0f / s;
+  int8_t* qr = q + row * ldq;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = (j * 64 + lane) * 8;
+    if (c < I) {
+      u32x2 o;
+      o.x = quant4(y[j][0], y[j][1], y[j][2], y[j][3], s, inv);
+      o.y = quant4(y[j][4], y[j][5], y[j][6], y[j][7], s, inv);
+      *reinterpret_cast<u32x2*>(qr + c) = o;
+    }
+  }
+  if (lane == 0) scale[row] = s;
+}
+
 }  // namespace
 
 hipError_t launch_repack_weights(const uint32_t* src, uint32_t* dst, int64_t n_words, int inverse, hipStream_t s) {
@@ -420,6 +474,14 @@ hipError_t launch_quant_rows(const uint16_t* x, int64_t ldx, int M, int K, int8_
 hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int P, int I, int8_t* q, int64_t ldq,
                                  float* scale, hipStream_t s) {
   if (P == 0) return hipSuccess;
+  const int cw = (I + 511) / 512;   // chunks per lane of a row per wave
+  if (cw <= 4) {
+    const dim3 g((P + kWaveRows - 1) / kWaveRows), b(64 * kWaveRows);
+    if (cw <= 1) hipLaunchKernelGGL(silu_mul_quant_wave_kernel<1>, g, b, 0, s, h, ldh, P, I, q, ldq, scale);
+    else if (cw <= 2) hipLaunchKernelGGL(silu_mul_quant_wave_kernel<2>, g, b, 0, s, h, ldh, P, I, q, ldq, scale);
+    else hipLaunchKernelGGL(silu_mul_quant_wave_kernel<4>, g, b, 0, s, h, ldh, P, I, q, ldq, scale);
+    return hipGetLastError();
+  }
   const int ch = row_chunks(I);
   const dim3 g(P), b(kRowThreads);
   if (ch <= 1) hipLaunchKernelGGL(silu_mul_quant_kernel<1>, g, b, 0, s, h, ldh, I, q, ldq, scale);
