@@ -298,7 +298,10 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
 
 // out[m, n] = bf16( sum_j w[m, j] * y[m * topk + j, n] ) with the products
 // and sums in fp32 in j order (w = 1 when weights is null). One thread per
-// 8 columns; N % 8 == 0.
+// 8 columns; N % 8 == 0. TK > 0: topk known at compile time, and a thread
+// issues all TK row loads before the first sum (TK == 0: a run-time loop
+// with one load in flight).
+template <int TK>
 __global__ __launch_bounds__(256) void combine_topk_kernel(const uint16_t* __restrict__ y, int64_t ldy, int topk,
                                                            int N, const float* __restrict__ weights,
                                                            uint16_t* __restrict__ out, int64_t ldo) {
@@ -308,9 +311,9 @@ __global__ __launch_bounds__(256) void combine_topk_kernel(const uint16_t* __res
   const int c = (blockIdx.x * 256 + threadIdx.x) * 8;
   if (c >= N) return;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < topk; ++j) {
+  auto add = [&](const u32x4 v, int j) {
     float f[8];
-    unpack8(*reinterpret_cast<const u32x4*>(y + (m * topk + j) * ldy + c), f);
+    unpack8(v, f);
     if (weights) {
       const float w = weights[m * topk + j];
 #pragma unroll
@@ -322,6 +325,15 @@ __global__ __launch_bounds__(256) void combine_topk_kernel(const uint16_t* __res
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] = acc[i] + f[i];
     }
+  };
+  if constexpr (TK > 0) {
+    u32x4 v[TK];
+#pragma unroll
+    for (int j = 0; j < TK; ++j) v[j] = *reinterpret_cast<const u32x4*>(y + (m * TK + j) * ldy + c);
+#pragma unroll
+    for (int j = 0; j < TK; ++j) add(v[j], j);
+  } else {
+    for (int j = 0; j < topk; ++j) add(*reinterpret_cast<const u32x4*>(y + (m * topk + j) * ldy + c), j);
   }
   u32x4 o;
   uint32_t b[8];
@@ -503,7 +515,15 @@ hipError_t launch_combine_topk(const uint16_t* y, int64_t ldy, int M, int topk, 
                                uint16_t* out, int64_t ldo, hipStream_t s) {
   if (M == 0) return hipSuccess;
   dim3 grid((N / 8 + 255) / 256, M);
-  hipLaunchKernelGGL(combine_topk_kernel, grid, dim3(256), 0, s, y, ldy, topk, N, weights, out, ldo);
+  const dim3 b(256);
+  switch (topk) {
+    case 1: hipLaunchKernelGGL(combine_topk_kernel<1>, grid, b, 0, s, y, ldy, topk, N, weights, out, ldo); break;
+    case 2: hipLaunchKernelGGL(combine_topk_kernel<2>, grid, b, 0, s, y, ldy, topk, N, weights, out, ldo); break;
+    case 4: hipLaunchKernelGGL(combine_topk_kernel<4>, grid, b, 0, s, y, ldy, topk, N, weights, out, ldo); break;
+    case 6: hipLaunchKernelGGL(combine_topk_kernel<6>, grid, b, 0, s, y, ldy, topk, N, weights, out, ldo); break;
+    case 8: hipLaunchKernelGGL(combine_topk_kernel<8>, grid, b, 0, s, y, ldy, topk, N, weights, out, ldo); break;
+    default: hipLaunchKernelGGL(combine_topk_kernel<0>, grid, b, 0, s, y, ldy, topk, N, weights, out, ldo); break;
+  }
   return hipGetLastError();
 }
 

@@ -105,7 +105,8 @@ def test_silu_mul_quant(pkg, dev, P, I):
 # ---------------------------------------------------------------- combine
 
 @pytest.mark.parametrize("M,topk,N,weighted", [(1, 1, 8, False), (64, 8, 7168, False), (33, 2, 4096, True),
-                                               (4096, 8, 2048, False)])
+                                               (4096, 8, 2048, False), (5, 3, 520, True), (7, 6, 1024, True),
+                                               (16, 8, 7168, True), (9, 4, 2056, False)])
 def test_combine_bit_exact(pkg, dev, M, topk, N, weighted):
     print(f"[combine] M={M} topk={topk} N={N} weighted={weighted}", flush=True)
     g = torch.Generator().manual_seed(M + N)
