@@ -249,12 +249,13 @@ def w4a8_fused_moe(x_q: torch.Tensor, x_scale: torch.Tensor, w_q4_packed: torch.
               f"routing buffers do not match block_m={block_m} (expected lengths {sl} and {bl})")
         _on_gpu(dict(sorted_ids=routing[0], expert_ids=routing[1], num_tokens_post_padded=routing[2]))
     L = _lib.lib()
-    stream = ctypes.c_void_p(_stream(dev))
+    sid = _stream(dev)
+    stream = ctypes.c_void_p(sid)
     if routing is None:
         # internal routing metadata: carved from the stream's cached int32
         # buffer (no allocation per call)
         sl, bl = align_buffer_sizes(P, E, block_m)
-        base = _routing_buffer(dev, stream.value, sl + bl + 1).data_ptr()
+        base = _routing_buffer(dev, sid, sl + bl + 1).data_ptr()
         sorted_p, expert_p, num_post_p = base, base + 4 * sl, base + 4 * (sl + bl)
         ids = topk_ids if topk_ids.is_contiguous() else topk_ids.contiguous()
         _lib.check(L.mw4a8_moe_align(_ptr(ids), P, E, block_m, sorted_p, expert_p, num_post_p, None, stream),
