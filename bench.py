@@ -347,7 +347,8 @@ def main():
             name, M = item.split(":")
             log(f"point {name} M={M}")
             pt = Point(pkg, name, int(M), dev)
-            points.append(measure_point(pt, max(args.steps, 20), args.warmup))
+            # side points: at least 10 warm-up and 50 timed calls (mean and median)
+            points.append(measure_point(pt, max(args.steps, 50), max(args.warmup, 10)))
             log(json.dumps(points[-1]))
             del pt
             torch.cuda.empty_cache()
@@ -356,7 +357,7 @@ def main():
     if not args.headline_only and not args.no_layer:
         for M in (int(m) for m in args.layers.split(",")):
             log(f"layer dsv3 M={M}")
-            layers.append(measure_layer(pkg, M, dev, max(args.steps, 20), args.warmup))
+            layers.append(measure_layer(pkg, M, dev, max(args.steps, 50), max(args.warmup, 10)))
             log(json.dumps(layers[-1]))
 
     if args.calibrate_copy:
