@@ -226,20 +226,24 @@ __global__ __launch_bounds__(kRowThreads) void silu_mul_quant_kernel(const uint1
 // (value desc, index asc) reduction. Softmax is monotonic, so these are the
 // top-k of the softmax; the weights are exp(l - l_max) normalised over the
 // chosen k (renormalize) or over all E.
-constexpr int kMaxPerLane = 16;
+constexpr int kMaxPerLane = 16;   // E <= 1024
 
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
+// CPL: 64-expert slots per lane, the smallest power of two >= E / 64 (each
+// of the k rounds scans only those)
+template <int CPL>
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int64_t ld, int M,
                                                           int E, int k, int renormalize, int32_t* __restrict__ ids,
                                                           float* __restrict__ weights) {
+  static_assert(CPL >= 1 && CPL <= kMaxPerLane, "experts per lane");
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (m >= M) return;   // whole wave leaves together
   const float* lr = logits + m * ld;
-  float v[kMaxPerLane];
+  float v[CPL];
 #pragma unroll
-  for (int j = 0; j < kMaxPerLane; ++j) {
+  for (int j = 0; j < CPL; ++j) {
     const int e = j * 64 + lane;
     v[j] = e < E ? lr[e] : -INFINITY;
   }
@@ -251,7 +255,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
     float bv = -INFINITY;
     int bi = 0x7fffffff;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
+    for (int j = 0; j < CPL; ++j) {
       const int e = j * 64 + lane;
       if (e < E && better(v[j], e, bv, bi)) {
         bv = v[j];
@@ -275,7 +279,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
       my_id = bi;
     }
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j)
+    for (int j = 0; j < CPL; ++j)
       if (j * 64 + lane == bi) v[j] = -INFINITY;
   }
   float denom = chosen_sum;
@@ -284,7 +288,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
     // cleared above, so add their terms back from chosen_sum)
     float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j)
+    for (int j = 0; j < CPL; ++j)
       if (j * 64 + lane < E && v[j] != -INFINITY) s += expf(v[j] - top_v);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
@@ -506,8 +510,13 @@ hipError_t launch_silu_mul_quant(const uint16_t* h, int64_t ldh, int P, int I, i
 hipError_t launch_router_topk(const float* logits, int64_t ld, int M, int E, int k, int renormalize, int32_t* ids,
                               float* weights, hipStream_t s) {
   if (M == 0) return hipSuccess;
-  hipLaunchKernelGGL(router_topk_kernel, dim3((M + 3) / 4), dim3(256), 0, s, logits, ld, M, E, k, renormalize,
-                     ids, weights);
+  const dim3 g((M + 3) / 4), b(256);
+  const int cpl = (E + 63) / 64;
+  if (cpl <= 1) hipLaunchKernelGGL(router_topk_kernel<1>, g, b, 0, s, logits, ld, M, E, k, renormalize, ids, weights);
+  else if (cpl <= 2) hipLaunchKernelGGL(router_topk_kernel<2>, g, b, 0, s, logits, ld, M, E, k, renormalize, ids, weights);
+  else if (cpl <= 4) hipLaunchKernelGGL(router_topk_kernel<4>, g, b, 0, s, logits, ld, M, E, k, renormalize, ids, weights);
+  else if (cpl <= 8) hipLaunchKernelGGL(router_topk_kernel<8>, g, b, 0, s, logits, ld, M, E, k, renormalize, ids, weights);
+  else hipLaunchKernelGGL(router_topk_kernel<16>, g, b, 0, s, logits, ld, M, E, k, renormalize, ids, weights);
   return hipGetLastError();
 }
 

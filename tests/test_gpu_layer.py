@@ -60,7 +60,8 @@ def test_quant_rows_strided_input(pkg, dev):
 # ---------------------------------------------------------------- router
 
 @pytest.mark.parametrize("M,E,k,renorm", [(1, 8, 2, True), (300, 256, 8, True), (77, 128, 8, False),
-                                          (33, 1024, 64, True), (40, 64, 1, True), (16, 5, 5, False)])
+                                          (33, 1024, 64, True), (40, 64, 1, True), (16, 5, 5, False),
+                                          (21, 512, 8, False), (9, 300, 6, True), (12, 200, 3, True)])
 def test_router_topk(pkg, dev, M, E, k, renorm):
     print(f"[router] M={M} E={E} k={k} renorm={renorm}", flush=True)
     g = torch.Generator().manual_seed(M * 7 + E)
