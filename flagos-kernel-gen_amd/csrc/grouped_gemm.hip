@@ -590,7 +590,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // chunk for all waves, as in the plain loop. Waves are placed round-robin
   // (w and w + 4 share a SIMD); of the groupings measured, late = waves 2, 3,
   // 6, 7 (each SIMD's two waves in the same order, two SIMDs each way) was
-  // fastest -- faster than the SIMD mates in opposite orders.
+  // fastest -- faster than the SIMD mates in opposite orders. A wave raises
+  // its issue priority for its compute phase, so that a SIMD mate's loads and
+  // staging fill the gaps rather than delay the MFMA chain (measured -0.75 %
+  // over five interleaved runs).
   constexpr bool STAGGER = NW == 8 && BMX == BM && RD == 2 && CLAMP;
   if constexpr (STAGGER) {
     // one interval of chunk cc (ring parity d); LATE selects the order
@@ -603,14 +606,18 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         }
       }
       if constexpr (LATE) {
+        __builtin_amdgcn_s_setprio(1);
         compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
+        __builtin_amdgcn_s_setprio(0);
         store_x((cc + 1) & 1);
         load_x(min(cc + 2, last_chunk));
         load_w(min(cc + 2, last_chunk), ring[d]);
       } else {
         load_x(min(cc + 1, last_chunk));
         load_w(min(cc + 1, last_chunk), ring[(d + 1) % 2]);
+        __builtin_amdgcn_s_setprio(1);
         compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
+        __builtin_amdgcn_s_setprio(0);
         store_x((cc + 1) & 1);
       }
       __syncthreads();
