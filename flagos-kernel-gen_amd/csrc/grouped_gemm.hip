@@ -924,10 +924,12 @@ static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   a.vec_out = (a.N % 8 == 0) && (a.ldo % 8 == 0) && (reinterpret_cast<uintptr_t>(a.out) % 16 == 0);
   // Expert groups pay a short search per tile; they pay off when an expert's
   // weights outgrow one XCD's 4 MB L2 (below that the weights stay cached
-  // across row blocks anyway). 128-row groups hold up to 4 blocks, 64-row
-  // groups 2 (set_grid has sized the grid for any grouping).
+  // across row blocks anyway). Groups hold up to 4 blocks (set_grid has
+  // sized the grid for any grouping). Measured on MI355X: with 128-row tiles
+  // 4 beat 2, 8 and 16 on the skewed DeepSeek-V3 point; with 64-row tiles 4
+  // beat 2 by 2.5 % on DeepSeek-V3 down M=4096 (up to 3 blocks an expert).
   a.egroups = RMODE != 0 && BM >= 64 && !DEBUGP && (int64_t)a.N * (a.K / 2) > (int64_t)4 << 20;
-  if (a.egroups) a.R = BM >= 128 ? 4 : 2;
+  if (a.egroups) a.R = 4;
   if (a.total_tiles == 0) return hipSuccess;
   // the guard-free body needs whole chunks, a chunk count divisible by the
   // unroll, and (without the LDS zero/scale block) aligned vector runs
