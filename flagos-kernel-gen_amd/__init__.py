@@ -8,7 +8,8 @@ Public API:
 * ``moe_align_block_size(topk_ids, block_m, num_experts)`` -- routing metadata.
 * ``w4a8_fused_moe(x_q, x_scale, w_q4_packed, w_scale, w_zero, topk_ids,
   topk_weights, group_size)`` -- routed GEMM with the top-k weight epilogue.
-* ``w4a8_group_partials`` -- debug export of the int32 group partial sums.
+* ``w4a8_group_partials`` / ``w4a8_fused_moe_partials`` -- debug exports of the
+  int32 group partial sums (reference layout / routed), from the product kernels.
 * ``repack_weights`` -- offline conversion to the MFMA weight order
   (``w4a8_fused_moe(..., weight_layout="mfma")``).
 * ``quant_per_token``, ``router_topk``, ``silu_mul_quant``, ``combine_topk``
@@ -19,7 +20,7 @@ module name ``flagos_kernel_gen_amd`` (see ``__graft_entry__.import_package``).
 """
 
 from .moe import (W4A8ShapeError, align_buffer_sizes, moe_align_block_size, repack_weights, select_block_m,
-                  w4a8_fused_moe, w4a8_group_gemm_moe, w4a8_group_partials)
+                  w4a8_fused_moe, w4a8_fused_moe_partials, w4a8_group_gemm_moe, w4a8_group_partials)
 from .layer import combine_topk, quant_per_token, router_topk, silu_mul_quant, w4a8_moe_layer
 from . import workloads
 
@@ -30,6 +31,7 @@ __all__ = [
     "repack_weights",
     "select_block_m",
     "w4a8_fused_moe",
+    "w4a8_fused_moe_partials",
     "w4a8_group_gemm_moe",
     "w4a8_group_partials",
     "workloads",

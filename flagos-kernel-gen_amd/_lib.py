@@ -26,6 +26,8 @@ SIGNATURES = {
     "mw4a8_fused_moe": (_i, [_p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _i64,
                              _i, _i, _i, _i, _i, _i, _p]),
     "mw4a8_debug_partials": (_i, [_p, _i64, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _sz, _p]),
+    "mw4a8_debug_partials_routed": (_i, [_p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _i64, _p,
+                                         _i, _i, _i, _i, _i, _i, _i, _p]),
     "mw4a8_fused_moe_repacked": (_i, [_p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _i64,
                                       _i, _i, _i, _i, _i, _i, _p]),
     "mw4a8_repack_weights": (_i, [_p, _p, _i64, _i, _i, _i, _p]),

@@ -20,7 +20,10 @@ LIB_NAME = "libmw4a8.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 ARCH = "gfx950"
 
-SOURCES = ("api.hip", "moe_align.hip", "grouped_gemm.hip", "moe_layer.hip")
+# the grouped GEMM's kernel template (gemm_kernel.h) is instantiated per row
+# source in the gemm_*.hip files, which compile in parallel
+SOURCES = ("gemm_routed.hip", "gemm_csr.hip", "gemm_repacked.hip", "gemm_debug_routed.hip", "gemm_debug_csr.hip",
+           "gemm_debug_repacked.hip", "api.hip", "moe_align.hip", "grouped_gemm.hip", "moe_layer.hip")
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -41,9 +44,16 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; the HIP toolchain is required to build libmw4a8.so")
 
 
+# The debug exports' extra stores make their fully unrolled loops larger than
+# the unroller's default limit for unroll pragmas; a higher limit keeps their
+# loop structure that of the product kernels.
+EXTRA_FLAGS = {src: ["-mllvm", "-pragma-unroll-threshold=200000"]
+               for src in ("gemm_debug_routed.hip", "gemm_debug_csr.hip", "gemm_debug_repacked.hip")}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), "-x", "hip", *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), "-x", "hip", *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
@@ -55,7 +65,7 @@ def _compile(src: str) -> str:
 
 def build(verbose: bool = True) -> str:
     os.makedirs(OBJ_DIR, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+    with ThreadPoolExecutor(max_workers=max(1, min(len(SOURCES), os.cpu_count() or 1))) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB_PATH + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]

@@ -76,13 +76,16 @@ CsrWorkspace carve(void* ws, int max_blocks) {
   return w;
 }
 
-GemmArgs base_args(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
+// rows >= 1 activation rows of K bytes, ldx apart: the kernels' activation
+// descriptor ends with the last row's K-th byte (not its row stride)
+GemmArgs base_args(const int8_t* x_q, int64_t ldx, int rows, const float* x_scale, const uint8_t* w_q4,
                    const float* w_scale, const int8_t* w_zero, uint16_t* out, int64_t ldo, int N, int K,
                    int gs) {
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   a.x = x_q;
   a.ldx = ldx;
+  a.x_bytes = (uint32_t)((int64_t)(rows - 1) * ldx + K);
   a.xs = x_scale;
   a.w = w_q4;
   a.ws = w_scale;
@@ -101,7 +104,8 @@ int run_csr(GemmArgs a, const int32_t* offsets, int M_total, int E, int gs, void
             hipStream_t s, bool debug) {
   if (!offsets) return fail(MW4A8_ERR_INVALID, "null expert_offsets");
   const int ne = E < M_total ? E : M_total;
-  TileConfig cfg = debug ? TileConfig{16, 16, 4, 512 / gs, 1} : select_tiles(M_total, ne, a.N, a.K, gs);
+  // the debug export runs the tile the product would select
+  const TileConfig cfg = select_tiles(M_total, ne, a.N, a.K, gs);
   const int max_blocks = max_row_blocks(M_total, E, cfg.BM);
   if (max_blocks == 0) return MW4A8_OK;
   if (!workspace || ws_bytes < csr_ws_bytes(max_blocks))
@@ -116,7 +120,8 @@ int run_csr(GemmArgs a, const int32_t* offsets, int M_total, int E, int gs, void
   a.blk_row0 = w.row0;
   a.blk_row1 = w.row1;
   a.blk_count = w.count;
-  e = debug ? launch_debug_partials(a, gs, max_blocks, s) : launch_grouped_gemm(a, cfg, gs, kModeCsr, max_blocks, s);
+  e = debug ? launch_debug_partials(a, cfg, gs, kModeCsr, max_blocks, s)
+            : launch_grouped_gemm(a, cfg, gs, kModeCsr, max_blocks, s);
   if (e != hipSuccess) return hip_fail(e, "grouped GEMM launch");
   return MW4A8_OK;
 }
@@ -146,8 +151,7 @@ int mw4a8_grouped_gemm(const int8_t* x_q, int64_t ldx, const float* x_scale, con
   int rc = check_gemm_args(x_q, ldx, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, M_total, N, K, E,
                            group_size, true);
   if (rc) return rc;
-  GemmArgs a = base_args(x_q, ldx, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, N, K, group_size);
-  a.x_bytes = (uint32_t)(M_total * ldx);
+  GemmArgs a = base_args(x_q, ldx, M_total, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, N, K, group_size);
   return run_csr(a, expert_offsets, M_total, E, group_size, workspace, ws_bytes,
                  static_cast<hipStream_t>(stream), false);
 }
@@ -160,9 +164,8 @@ int mw4a8_debug_partials(const int8_t* x_q, int64_t ldx, const uint8_t* w_q4, co
   int rc = check_gemm_args(x_q, ldx, nullptr, w_q4, nullptr, w_zero, partials, N, M_total, N, K, E,
                            group_size, false);
   if (rc) return rc;
-  GemmArgs a = base_args(x_q, ldx, nullptr, w_q4, nullptr, w_zero, nullptr, N, N, K, group_size);
+  GemmArgs a = base_args(x_q, ldx, M_total, nullptr, w_q4, nullptr, w_zero, nullptr, N, N, K, group_size);
   a.dbg = partials;
-  a.x_bytes = (uint32_t)(M_total * ldx);
   return run_csr(a, expert_offsets, M_total, E, group_size, workspace, ws_bytes,
                  static_cast<hipStream_t>(stream), true);
 }
@@ -206,7 +209,8 @@ namespace {
 int fused_moe_impl(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4, const float* w_scale,
                    const int8_t* w_zero, const int32_t* sorted_ids, const int32_t* expert_ids,
                    const int32_t* num_post_pad, const float* topk_weights, int topk, uint16_t* out_bf16, int64_t ldo,
-                   int M, int N, int K, int E, int group_size, int block_m, int mode, void* stream) {
+                   int M, int N, int K, int E, int group_size, int block_m, int mode, void* stream,
+                   int32_t* partials = nullptr) {
   g_err[0] = 0;
   if (topk <= 0) return fail(MW4A8_ERR_INVALID, "topk=%d", topk);
   if (M == 0) return MW4A8_OK;
@@ -219,8 +223,7 @@ int fused_moe_impl(const int8_t* x_q, int64_t ldx, const float* x_scale, const u
     return fail(MW4A8_ERR_UNSUPPORTED, "block_m=%d not in {16,32,64,128}", block_m);
   const int64_t pairs = (int64_t)M * topk;
   if (pairs > 0x7fffffff / 2) return fail(MW4A8_ERR_UNSUPPORTED, "too many pairs");
-  GemmArgs a = base_args(x_q, ldx, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, N, K, group_size);
-  a.x_bytes = (uint32_t)(M * ldx);
+  GemmArgs a = base_args(x_q, ldx, M, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, N, K, group_size);
   a.sorted_ids = sorted_ids;
   a.expert_ids = expert_ids;
   a.num_post_pad = num_post_pad;
@@ -236,7 +239,9 @@ int fused_moe_impl(const int8_t* x_q, int64_t ldx, const float* x_scale, const u
   const TileConfig cfg = tiles_for_block_m(block_m, group_size);
   if (cfg.BM != block_m) return fail(MW4A8_ERR_UNSUPPORTED, "block_m must be 16, 32, 64 or 128");
   const int max_blocks = max_row_blocks((int)pairs, E, block_m);
-  hipError_t e = launch_grouped_gemm(a, cfg, group_size, mode, max_blocks, static_cast<hipStream_t>(stream));
+  a.dbg = partials;
+  hipError_t e = partials ? launch_debug_partials(a, cfg, group_size, mode, max_blocks, static_cast<hipStream_t>(stream))
+                          : launch_grouped_gemm(a, cfg, group_size, mode, max_blocks, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "fused MoE launch");
   return MW4A8_OK;
 }
@@ -262,6 +267,19 @@ int mw4a8_fused_moe_repacked(const int8_t* x_q, int64_t ldx, const float* x_scal
   return fused_moe_impl(x_q, ldx, x_scale, w_mfma, w_scale, w_zero, sorted_ids, expert_ids, num_post_pad,
                         topk_weights, topk, out_bf16, ldo, M, N, K, E, group_size, block_m, kModeRoutedRepacked,
                         stream);
+}
+
+int mw4a8_debug_partials_routed(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
+                                const float* w_scale, const int8_t* w_zero, const int32_t* sorted_ids,
+                                const int32_t* expert_ids, const int32_t* num_post_pad, const float* topk_weights,
+                                int topk, uint16_t* out_bf16, int64_t ldo, int32_t* partials, int M, int N, int K,
+                                int E, int group_size, int block_m, int repacked, void* stream) {
+  g_err[0] = 0;
+  if (!partials) return fail(MW4A8_ERR_INVALID, "null partials");
+  if (!aligned(partials, 4)) return fail(MW4A8_ERR_INVALID, "misaligned partials");
+  return fused_moe_impl(x_q, ldx, x_scale, w_q4, w_scale, w_zero, sorted_ids, expert_ids, num_post_pad,
+                        topk_weights, topk, out_bf16, ldo, M, N, K, E, group_size, block_m,
+                        repacked ? kModeRoutedRepacked : kModeRouted, stream, partials);
 }
 
 int mw4a8_repack_weights(const uint8_t* src, uint8_t* dst, int64_t E, int N, int K, int inverse, void* stream) {
@@ -439,6 +457,75 @@ int mw4a8_host_selftest(void) {
     }
     for (int i = 0; i < nblocks * n_tiles; ++i) bad += seen[i] != 1;
   }
+  // an expert_ids table that is not ascending (not what moe_align writes):
+  // the grouped order may skip tiles, but never pairs a block with another
+  // expert's weights
+  for (int trial = 0; trial < 300; ++trial) {
+    int32_t ids[64];
+    const int nblocks = 1 + (int)(rnd() % 64), E = 1 + (int)(rnd() % 8);
+    for (int i = 0; i < nblocks; ++i) ids[i] = (int)(rnd() % (E + 1)) - (rnd() % 8 == 0 ? 1 : 0);
+    const int R = 1 + (int)(rnd() % 4), n_tiles = 1 + (int)(rnd() % 5);
+    for (int t = 0; t < nblocks * n_tiles; ++t) {
+      int b = -1, nt = -1, ex = -1;
+      if (expert_group_tile(t, n_tiles, R, nblocks, ids, E, b, nt, ex))
+        bad += b < 0 || b >= nblocks || nt < 0 || nt >= n_tiles || ids[b] != ex;
+    }
+  }
+  // weight loads (w_lane_offset + w_group_soffset, as the kernel forms them):
+  // for every group size, chunk length and group count the dispatcher can
+  // use, every piece a lane loads -- including the groups past the last one
+  // that a partial last chunk requests -- lies inside the expert's [N, K/2]
+  // slice, and the pieces of a group gg < G tile exactly its GS/2 bytes of
+  // its column
+  for (int GS = 64; GS <= 256; GS *= 2) {
+    const int piece = GS == 64 ? 8 : 16, pieces = GS == 64 ? 1 : GS / 128;
+    for (int KCG = 1; KCG <= 16; KCG *= 2)
+      for (int G = 1; G <= 72; ++G)
+        for (int N = 1; N <= 3; ++N) {
+          const uint32_t khalf = (uint32_t)(G * GS / 2), slice = (uint32_t)N * khalf;
+          const int nchunks = (G + KCG - 1) / KCG;
+          for (int gg = 0; gg < nchunks * KCG; ++gg)
+            for (int col = 0; col < N; ++col) {
+              uint8_t cover[128];
+              memset(cover, 0, sizeof(cover));
+              for (int kb = 0; kb < 4; ++kb)
+                for (int h = 0; h < pieces; ++h) {
+                  const uint32_t start =
+                      w_lane_offset(col, khalf, kb, GS) + 16u * h + (uint32_t)w_group_soffset(gg, G, GS);
+                  bad += start + piece > slice;
+                  if (gg < G) {
+                    const uint32_t g0 = (uint32_t)col * khalf + (uint32_t)(gg * GS / 2);
+                    if (start < g0 || start + piece > g0 + GS / 2) {
+                      ++bad;
+                    } else {
+                      for (int i = 0; i < piece; ++i) cover[start - g0 + i]++;
+                    }
+                  }
+                }
+              if (gg < G)
+                for (int i = 0; i < GS / 2; ++i) bad += cover[i] != 1;
+            }
+        }
+  }
+  // activation chunks: the descriptor of chunk ch starts at ch * KC and ends
+  // where the tensor ends ((rows - 1) * ldx + K bytes); every unit of real
+  // data (k < K) of every row reads inside it, so none is zeroed by the
+  // range check
+  for (int GS = 64; GS <= 256; GS *= 2)
+    for (int KCG = 1; KCG <= 16; KCG *= 2)
+      for (int G = 1; G <= 40; ++G)
+        for (int rows = 1; rows <= 3; ++rows)
+          for (int pad = 0; pad <= 64; pad += 16) {
+            const int K = G * GS, KC = KCG * GS, ldx = K + pad;
+            const int64_t x_bytes = (int64_t)(rows - 1) * ldx + K;
+            for (int ch = 0; ch * KC < K; ++ch) {
+              const int64_t size = x_bytes - (int64_t)ch * KC;
+              bad += size <= 0;
+              for (int r = 0; r < rows; ++r)
+                for (int cu = 0; cu < KC / 16; ++cu)
+                  if (ch * KC + cu * 16 < K) bad += (int64_t)r * ldx + cu * 16 + 16 > size;
+            }
+          }
   // bf16 round to nearest even
   struct Case { uint32_t in; uint16_t out; };
   const Case cases[] = {

@@ -1,0 +1,10 @@
+// Instantiations of the grouped-GEMM kernel: debug export of the int32 group partials, routed pairs on repacked weights.
+#include "gemm_kernel.h"
+
+namespace mw4a8 {
+
+template hipError_t dispatch_bm<64, kModeRoutedRepacked, true>(GemmArgs, const TileConfig&, int, hipStream_t);
+template hipError_t dispatch_bm<128, kModeRoutedRepacked, true>(GemmArgs, const TileConfig&, int, hipStream_t);
+template hipError_t dispatch_bm<256, kModeRoutedRepacked, true>(GemmArgs, const TileConfig&, int, hipStream_t);
+
+}  // namespace mw4a8

@@ -1,0 +1,1014 @@
+// W4A8 grouped GEMM for gfx950 (int8 MFMA, int32 accumulation per K-group).
+//
+// One workgroup computes a BM x BN output tile for one expert. Its waves
+// split the BN columns (WN columns each) and all share the BM activation
+// rows, which are staged through LDS once per K-chunk. Each wave streams its
+// own packed int4 weight columns straight from HBM into registers with
+// 128-bit buffer loads (four lanes cover the 64 contiguous bytes of one
+// column's 128-wide K-group), unpacks them to int8 with the zero point folded
+// in (mw4a8_pack.h), and feeds v_mfma_i32_16x16x64_i8.
+//
+// Per K-group and 16-row block the int32 MFMA results start from zero; right
+// after the block's MFMAs they are converted to fp32 and multiplied by the
+// group scale into the fp32 accumulator (docs/Task1.md:99-107, int32 per
+// group as the reference's Hygon kernel does it). The epilogue multiplies by
+// the per-row activation scale and, for routed launches, the top-k routing
+// weight, rounds to bf16 and stores the row (docs/Task1.md:109-112).
+//
+// Memory access is branch-free: every global read is a raw buffer load whose
+// descriptor covers exactly the tensor (or one expert's slice of it), and
+// lanes with nothing to read (padding rows, columns past N) use an offset
+// beyond the descriptor, which the hardware returns as zero. A tile whose
+// valid rows fit in its top half runs a half-height body, so a nearly empty
+// last row block of an expert costs at most half a tile of MFMAs.
+//
+// Pipelining: the activation chunk and the weight registers of chunk c+1 are
+// requested before chunk c is computed. Weights ping-pong between two
+// register sets (the loop is unrolled by two chunks, so no copies), and LDS
+// is double-buffered, so one barrier per chunk suffices.
+//
+// Grid: a 1-D list of (row block, column tile) pairs, sized on the host for
+// the worst-case number of row blocks. Workgroup L runs on XCD L % 8; with
+// per_xcd = ceil(actual tiles / 8), tile t = (L % 8) * per_xcd + L / 8 gives
+// every XCD an equal, contiguous run of the actual tiles. The list walks R row blocks
+// (usually of one expert) across all column tiles before moving on, so the
+// activation rows and the weight tile a row block pair shares stay in that
+// XCD's L2.
+//
+// Memory safety of the loads: the hardware range check of a raw buffer load
+// covers its vector offset, not the scalar one. Every scalar offset here
+// therefore stays inside the tensor by construction: weight groups past the
+// last one (a partial last K-chunk) are clamped to the last group, and the
+// activation chunk offset moves the descriptor's base (and shrinks its
+// size) instead of travelling as a scalar offset, so the range check still
+// covers the end of the activation tensor.
+//
+// This header holds the kernel template and its launch helpers; each
+// gemm_*.hip file instantiates dispatch_bm for one row source.
+#pragma once
+#include <type_traits>
+
+#include "mw4a8_internal.h"
+#include "mw4a8_pack.h"
+
+namespace mw4a8 {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t kOOB = 0x80000000u;   // buffer offset that reads as zero
+// float bits of 12582912 = 1.5 * 2^23: adding an integer P with |P| <= 2^22 to
+// them gives the float 12582912 + P exactly
+constexpr int kMagic = 0x4B400000;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+// two fp32 -> packed bf16 (a low, b high), round to nearest even: one
+// v_cvt_pk_bf16_f32 (same bits as bf16_rne_bits for every non-NaN input)
+__device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+constexpr float kMagicF = 12582912.0f;
+constexpr int kRsrcFlags = 0x00020000;   // raw buffer, 32-bit data format
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcFlags);
+}
+
+// KCG consecutive int8 zero points at byte offset `off` (KCG-aligned), kept
+// as raw words (zero point g is byte g % 4 of w[g / 4]). They are
+// sign-extended where they are used (zero_of), not here: extracting them
+// right after the load would make the wave wait for the load, and with it
+// for every load issued before it.
+template <int KCG>
+__device__ __forceinline__ void load_zero_run(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t (&w)[(KCG + 3) / 4]) {
+  if constexpr (KCG == 1) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+  } else if constexpr (KCG == 2) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  } else if constexpr (KCG == 4) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  } else if constexpr (KCG == 8) {
+    const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    w[0] = q.x;
+    w[1] = q.y;
+  } else {
+    static_assert(KCG % 16 == 0, "zero-point run length");
+#pragma unroll
+    for (int h = 0; h < KCG / 16; ++h) {
+      const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * h, 0, 0);
+      w[4 * h] = q.x;
+      w[4 * h + 1] = q.y;
+      w[4 * h + 2] = q.z;
+      w[4 * h + 3] = q.w;
+    }
+  }
+}
+
+template <int KCG>
+__device__ __forceinline__ int zero_of(const uint32_t (&w)[(KCG + 3) / 4], int g) {
+  return (int)(int8_t)((w[g / 4] >> (8 * (g % 4))) & 0xffu);
+}
+
+// KCG consecutive fp32 scales at byte offset `off` (4*KCG-aligned up to 16).
+template <int KCG, int NB>
+__device__ __forceinline__ void load_scale_run(__amdgpu_buffer_rsrc_t r, uint32_t off, float (&dst)[KCG][NB],
+                                               int nb) {
+  if constexpr (KCG == 1) {
+    dst[0][nb] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  } else if constexpr (KCG == 2) {
+    const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    dst[0][nb] = __uint_as_float(q.x);
+    dst[1][nb] = __uint_as_float(q.y);
+  } else {
+    static_assert(KCG % 4 == 0, "scale run length");
+#pragma unroll
+    for (int h = 0; h < KCG / 4; ++h) {
+      const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * h, 0, 0);
+      dst[4 * h][nb] = __uint_as_float(q.x);
+      dst[4 * h + 1][nb] = __uint_as_float(q.y);
+      dst[4 * h + 2][nb] = __uint_as_float(q.z);
+      dst[4 * h + 3][nb] = __uint_as_float(q.w);
+    }
+  }
+}
+
+// ---- LDS layout of the staged activations ---------------------------------
+// ds_read_b128 / ds_write_b128 are served 32 lanes per cycle across 128
+// four-byte banks, i.e. 32 sixteen-byte segments: a cycle is conflict-free
+// when its 32 lanes touch 32 distinct segments (mod 32).
+//
+// Rows are PITCH = KC + 32 bytes apart, so PITCH / 16 = 2 * odd and the 16
+// rows of an MFMA A fragment start on 16 distinct even segments. Within a
+// K-group, the 16-byte unit that K slot kb of MFMA step s reads (K-order unit
+// kb * S + s) is stored at position 4 * s + kb; lanes 0-31 (kb = 0, 1) then
+// read 32 distinct segments for every s.
+//
+// Stores: a 32-lane half writes 32 / UPR rows (UPR 16-byte units per row).
+// Rows r and r + XD, with (PITCH / 16) * XD = UPR (mod 32), land on disjoint
+// segment ranges, so each half writes such rows: row_of_group() maps the
+// q-th row group of the thread order to a row, bijectively within every 16
+// rows.
+__host__ __device__ constexpr int lds_row_step(int upr) {
+  int d = 1;
+  while (d < 32 && ((upr + 2) * d) % 32 != upr % 32) ++d;
+  return d;
+}
+
+template <int UPR>
+__device__ __forceinline__ int row_of_group(int q) {
+  if constexpr (UPR >= 32) {
+    return q;
+  } else {
+    constexpr int XR = 32 / UPR;            // rows per 32-lane half
+    constexpr int XD = lds_row_step(UPR);   // row distance within a half
+    static_assert(XR * XD == 16, "row interleave must tile 16 rows");
+    const int j = q % XR, b = q / XR;
+    return (b % XD) + XD * j + 16 * (b / XD);
+  }
+}
+
+// LDS byte position of K-order unit cu (16 bytes) within a row's chunk.
+template <int GS>
+__device__ __forceinline__ int unit_pos(int cu) {
+  constexpr int S = GS / 64, UG = GS / 16;
+  const int g = cu / UG, v = cu - g * UG;
+  return 16 * (g * UG + (v % S) * 4 + v / S);
+}
+
+// Chunks per zero-point/scale window (ZSV): the window's runs are read with
+// one vector load each per column block. RD chunks (the loop's unroll) while
+// the window's scales fit in 8 registers, else one chunk.
+__host__ __device__ constexpr int zs_window(int kcg, int rd) { return kcg * rd <= 8 ? rd : 1; }
+
+// Per-tile values shared by the kernel's setup and its tile bodies.
+struct TileCtx {
+  int e;          // expert
+  int col0;       // first column of this wave
+  int tile_col0;  // first column of the workgroup's tile
+  int nchunks;    // K-chunks
+  int rows;       // rows of the tile holding data (the rest is padding)
+};
+
+// Main K loop and epilogue for the first BMX rows of a tile (BMX <= BM).
+//
+// RD: weight-register ring depth. The weights (and, unless ZS_LDS, the zero
+//     points and scales) of chunk c + RD - 1 are requested while chunk c is
+//     computed.
+// ZSG: when positive, the tile's whole [BN x G] zero-point and scale block
+//     (G <= ZSG) is copied into LDS once -- it is contiguous in memory -- so
+//     the K loop issues no loads for them. When zero they travel with the
+//     weights, one vector run per column and chunk when aligned.
+// FAST: the host guarantees that every chunk is full and the chunk count is
+//     a multiple of RD (G % (KCG * RD) == 0) and, without ZSG, that the
+//     zero-point / scale runs are aligned; the loop then carries no guards.
+//     (Used for the 16- and 32-row tiles only: without the guards the
+//     compiler schedules the larger bodies into scratch.)
+// ZSV (ZSG == 0 only): the zero points and scales of a window of
+//     zs_window(KCG, RD) chunks are read as one aligned vector run each per
+//     column (host-checked: G a multiple of the window's groups, 16-byte
+//     aligned tensors); otherwise one scalar load per group and chunk. Every
+//     such load costs the memory pipeline about as much as a 1 KB weight
+//     load (each touches one cache line per column), so fewer, wider runs
+//     leave more of it to the weights. It is a compile-time choice so that
+//     the loads of the next chunk lie on one straight path: with a run-time
+//     choice the compiler copied the loaded registers where the two paths
+//     join, and waited there for every outstanding load, which serialized
+//     the prefetch with the compute.
+template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST,
+          bool ZSV, bool SYMT>
+__device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, int8_t* s_x, float* s_scale,
+                                          int8_t* s_zero, const int* s_src, const int* s_dst, const float* s_xs,
+                                          const float* s_tw) {
+  constexpr int NT = NW * 64;
+  constexpr int MB = BMX / 16;        // 16-row blocks computed
+  constexpr int NB = WN / 16;         // 16-column blocks per wave
+  constexpr int BN = NW * WN;
+  constexpr int S = GS / 64;          // MFMA K-steps per group
+  constexpr int WD = 2 * S;           // packed dwords per lane per (group, column block)
+  constexpr int KC = KCG * GS;        // activation bytes per row per chunk
+  constexpr int PITCH = KC + 32;      // LDS row pitch in bytes (see the layout note)
+  constexpr int BUF = BM * PITCH;     // bytes per LDS buffer
+  constexpr int UPR = KC / 16;        // 16-byte units per row and chunk
+  constexpr int XU = (BMX * UPR + NT - 1) / NT;
+  constexpr bool ZS_LDS = ZSG > 0;
+  constexpr bool ROUTED = RMODE != 0;
+  constexpr bool REPACKED = RMODE == kModeRoutedRepacked;
+  // SYMT: every zero point of the tile is 8 (decided by the kernel entry for
+  // tiles with an LDS zero/scale block): symmetric unpack and magic-number
+  // fold for every group, scales stored / 16, no zero points needed.
+  // DEBUGP changes none of the arithmetic: the same body also writes each
+  // exact int32 group partial (decoded from its chain, see fold) to a.dbg.
+  constexpr bool MG = SYMT && ZS_LDS;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int jl = lane & 15;   // row (A) / column (B) within a 16-block
+  const int kb = lane >> 4;   // K slot group of the MFMA operands
+  const uint32_t khalf = (uint32_t)a.K / 2;
+
+  // ---- buffer descriptors (one expert's slice for the weights) ------------
+  const int64_t expert_cols = (int64_t)c.e * a.N;
+  const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w + expert_cols * khalf, (uint32_t)a.N * khalf);
+  const __amdgpu_buffer_rsrc_t z_rsrc = make_rsrc(a.wz + expert_cols * a.G, (uint32_t)(a.N * a.G));
+  // the reference-layout debug export passes no scales: an empty descriptor
+  // (every scale reads as zero) keeps its loop identical to the product's
+  const __amdgpu_buffer_rsrc_t s_rsrc =
+      (DEBUGP && a.ws == nullptr) ? make_rsrc(a.wz, 0u)
+                                  : make_rsrc(a.ws + expert_cols * a.G, (uint32_t)(a.N * a.G) * 4u);
+
+  // per-lane offsets of this lane's weight columns and activation units
+  uint32_t w_off[NB], zs_off[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int col = c.col0 + nb * 16 + jl;
+    const bool ok = col < a.N;
+    w_off[nb] = ok ? w_lane_offset(col, khalf, kb, GS) : kOOB;
+    zs_off[nb] = ok ? (uint32_t)(col * a.G) : kOOB;
+  }
+  // Padding rows read zeros (out-of-range offset) and are staged like the
+  // others, which keeps the staging loops free of per-lane branches; their
+  // results are never stored.
+  static_assert((BMX * UPR) % NT == 0, "staging units must divide evenly over the threads");
+  uint32_t x_off[XU];
+  int x_lds[XU];   // LDS byte offset within a buffer
+#pragma unroll
+  for (int j = 0; j < XU; ++j) {
+    const int u = tid + j * NT;
+    const int q = u / UPR;
+    const int cu = u - q * UPR;
+    const int row = row_of_group<UPR>(q);
+    const int src = s_src[row];
+    x_off[j] = src >= 0 ? (uint32_t)(src * a.ldx) + (uint32_t)(cu * 16) : kOOB;
+    x_lds[j] = row * PITCH + unit_pos<GS>(cu);
+  }
+
+  // ---- the tile's zero points and scales -> registers (ZS_LDS) -------------
+  // [BN columns x G] of each, contiguous from column tile_col0; the
+  // descriptors return zero past column N. All loads are issued before any
+  // LDS write so their latencies overlap (and overlap the pipeline prologue).
+  constexpr int SU = ZS_LDS ? (BN * ZSG / 4 + NT - 1) / NT : 1;    // scale units per thread
+  constexpr int ZU = ZS_LDS ? (BN * ZSG / 16 + NT - 1) / NT : 1;   // zero-point units per thread
+  const int s_units = BN * a.G / 4;
+  const int z_units = BN * a.G / 16;
+  u32x4 sq[SU], zq[ZU];
+  if constexpr (ZS_LDS) {
+    const uint32_t zbase = (uint32_t)(c.tile_col0 * a.G);
+#pragma unroll
+    for (int j = 0; j < SU; ++j) {
+      const int u = tid + j * NT;
+      if (u < s_units) sq[j] = __builtin_amdgcn_raw_buffer_load_b128(s_rsrc, zbase * 4u + u * 16u, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < ZU; ++j) {
+      const int u = tid + j * NT;
+      if (!MG && u < z_units) zq[j] = __builtin_amdgcn_raw_buffer_load_b128(z_rsrc, zbase + u * 16u, 0, 0);
+    }
+  }
+  // LDS index of this lane's columns in the zero/scale block
+  int zs_lds[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) zs_lds[nb] = (c.col0 - c.tile_col0 + nb * 16 + jl) * a.G;
+
+  // ---- chunk loaders -----------------------------------------------------
+  u32x4 xr[XU];
+  // the chunk's K offset moves the descriptor (scalar work) rather than going
+  // into the unchecked scalar offset: units past K in a partial last chunk of
+  // the tensor's last row then read as zero instead of past its end
+  auto load_x = [&](int ch) {
+    const uint32_t base = (uint32_t)(ch * KC);
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(a.x + base, a.x_bytes - base);
+#pragma unroll
+    for (int j = 0; j < XU; ++j) xr[j] = __builtin_amdgcn_raw_buffer_load_b128(r, x_off[j], 0, 0);
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < XU; ++j) {
+      const u32x4 v = xr[j];
+      if constexpr (REPACKED) {
+        // the repacked weights unpack in natural K order: no relabel
+        *reinterpret_cast<u32x4*>(s_x + buf * BUF + x_lds[j]) = v;
+      } else {
+        u32x4 p;
+        p.x = even_bytes(v.x, v.y);
+        p.y = odd_bytes(v.x, v.y);
+        p.z = even_bytes(v.z, v.w);
+        p.w = odd_bytes(v.z, v.w);
+        *reinterpret_cast<u32x4*>(s_x + buf * BUF + x_lds[j]) = p;
+      }
+    }
+  };
+
+  struct WChunk {
+    uint32_t w[KCG][NB][WD];
+    int z[KCG][NB];     // !ZSV: sign-extended zero points
+    float s[KCG][NB];   // !ZSV: scales
+  };
+  // ZSV: one window of ZW chunks (KW groups) of zero points (raw runs) and scales
+  constexpr int ZW = zs_window(KCG, RD);
+  constexpr int KW = ZW * KCG;
+  struct ZsWin {
+    uint32_t zr[NB][(KW + 3) / 4];
+    float s[KW][NB];
+  };
+  auto load_zs = [&](int win, ZsWin& d) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const uint32_t zo = zs_off[nb] + (uint32_t)(win * KW);
+      load_zero_run<KW>(z_rsrc, zo, d.zr[nb]);
+      load_scale_run<KW, NB>(s_rsrc, zo * 4u, d.s, nb);
+    }
+  };
+  auto load_w = [&](int ch, WChunk& d) {
+#pragma unroll
+    for (int g = 0; g < KCG; ++g) {
+      const uint32_t gg = (uint32_t)(ch * KCG + g);
+      // groups past the last one (partial last chunk; never computed) load
+      // the last group again, so the scalar offset stays inside the column
+      const int soff = w_group_soffset((int)gg, a.G, GS);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint32_t off = w_off[nb];
+        if constexpr (S == 1) {
+          const u32x2 q = __builtin_amdgcn_raw_buffer_load_b64(w_rsrc, off, soff, 0);
+          d.w[g][nb][0] = q.x;
+          d.w[g][nb][1] = q.y;
+        } else {
+#pragma unroll
+          for (int h = 0; h < S / 2; ++h) {
+            const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, off + 16 * h, soff, 0);
+            d.w[g][nb][4 * h + 0] = q.x;
+            d.w[g][nb][4 * h + 1] = q.y;
+            d.w[g][nb][4 * h + 2] = q.z;
+            d.w[g][nb][4 * h + 3] = q.w;
+          }
+        }
+        if constexpr (!ZS_LDS && !ZSV) {
+          d.z[g][nb] = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(z_rsrc, zs_off[nb] + gg, 0, 0);
+          d.s[g][nb] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(s_rsrc, (zs_off[nb] + gg) * 4u, 0, 0));
+        }
+      }
+    }
+  };
+
+  float acc[MB][NB][4];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[mb][nb][r] = 0.f;
+  const i32x4 magic4 = {kMagic, kMagic, kMagic, kMagic};
+
+  // ---- one chunk of K ------------------------------------------------------
+  // dd: position of the chunk in its zero/scale window (compile-time after unrolling)
+  //
+  // Fold without a convert: each group's MFMA chain starts from the integer
+  // kMagic = 0x4B400000 instead of 0, so the int32 result M + P (|P| <= 2^22
+  // for every group size here) read as a float is exactly 12582912 + P. One
+  // FMA then folds (12582912 + P) * s; the 12582912 * s of the groups is
+  // summed per column (bias) and subtracted from the accumulators every RD
+  // chunks (rebase), which keeps their magnitude, and the extra rounding,
+  // small. Only symmetric tiles with an LDS zero/scale block (SYMT: scales
+  // / 16, so a small bias) take this path; every other tile and kernel
+  // keeps the plain int32 chain and a convert.
+  float bias[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) bias[nb] = 0.f;
+  auto rebase = [&]() {
+    if constexpr (MG) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[mb][nb][r] -= bias[nb];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) bias[nb] = 0.f;
+    }
+  };
+  auto compute = [&](int ch, const int8_t* xb, const WChunk& wc, const ZsWin& zw, int dd) {
+#pragma unroll
+    for (int g = 0; g < KCG; ++g) {
+      const int gg = ch * KCG + g;
+      if (FAST || gg < a.G) {
+        int zv[NB];
+        float sv[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          if constexpr (ZS_LDS) {
+            zv[nb] = s_zero[zs_lds[nb] + gg];
+            sv[nb] = s_scale[zs_lds[nb] + gg];
+          } else if constexpr (ZSV) {
+            zv[nb] = zero_of<KW>(zw.zr[nb], dd * KCG + g);
+            sv[nb] = zw.s[dd * KCG + g][nb];
+          } else {
+            zv[nb] = wc.z[g][nb];
+            sv[nb] = wc.s[g][nb];
+          }
+        }
+        i32x4 bfr[NB][S];
+        // Symmetric int4 (every zero point of the tile -- LDS block -- or of
+        // this group in the wave is 8):
+        // 16 * (u - 8) is the nibble with its top bit flipped, moved into the
+        // high half of its byte, so unpacking takes 1.5 ops per int8 dword
+        // instead of 3.5. The partials come out 16x larger and the scale is
+        // used / 16; both factors are powers of two, so the product fed to
+        // the fold is the same real number.
+        bool sym = false;
+        if constexpr (MG) {
+          sym = true;   // scales already / 16
+        } else {
+          bool z8 = true;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) z8 = z8 && zv[nb] == 8;
+          sym = __all(z8);
+        }
+        if (sym) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            if constexpr (!MG) sv[nb] *= 0.0625f;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+              // the top-bit flip (repacked weights store it) is applied after
+              // the mask, so each half is a shift and one 3-input op
+              const uint32_t flip = REPACKED ? 0u : 0x80808080u;
+              const uint32_t t0 = wc.w[g][nb][2 * s];
+              const uint32_t t1 = wc.w[g][nb][2 * s + 1];
+              bfr[nb][s].x = (int)(((t0 << 4) & 0xF0F0F0F0u) ^ flip);
+              bfr[nb][s].y = (int)((t0 & 0xF0F0F0F0u) ^ flip);
+              bfr[nb][s].z = (int)(((t1 << 4) & 0xF0F0F0F0u) ^ flip);
+              bfr[nb][s].w = (int)((t1 & 0xF0F0F0F0u) ^ flip);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const ZeroFold zf = make_zero_fold(zv[nb]);
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+              const uint32_t flip = REPACKED ? 0x88888888u : 0u;
+              const uint32_t d0 = wc.w[g][nb][2 * s] ^ flip;
+              const uint32_t d1 = wc.w[g][nb][2 * s + 1] ^ flip;
+              bfr[nb][s].x = (int)fold_even(d0, zf);
+              bfr[nb][s].y = (int)fold_odd(d0, zf);
+              bfr[nb][s].z = (int)fold_even(d1, zf);
+              bfr[nb][s].w = (int)fold_odd(d1, zf);
+            }
+          }
+        }
+        if constexpr (MG) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) bias[nb] = __builtin_fmaf(kMagicF, sv[nb], bias[nb]);
+        }
+        // Software-pipelined over 16-row blocks: the A fragments of block
+        // mb+1 are read from LDS while block mb's MFMAs run, and block mb-1's
+        // int32 partials are folded into the fp32 accumulators after block
+        // mb's MFMAs are issued, so neither the LDS latency nor the MFMA
+        // result latency sits on the issue path.
+        const int8_t* xg = xb + jl * PITCH + g * GS + kb * 16;
+        auto read_a = [&](int mb, i32x4 (&av)[S]) {
+#pragma unroll
+          for (int s = 0; s < S; ++s) av[s] = *reinterpret_cast<const i32x4*>(xg + mb * 16 * PITCH + 64 * s);
+        };
+        auto fold = [&](int mb, const i32x4 (&part)[NB]) {
+          if constexpr (DEBUGP) {
+            // the exact partial from the chain's value: minus the seed on
+            // magic-seeded chains, / 16 (exact) after the symmetric unpack
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+              const int col = c.col0 + nb * 16 + jl;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int dst = s_dst[mb * 16 + kb * 4 + r];
+                int p = part[nb][r];
+                if constexpr (MG) p -= kMagic;
+                if (sym) p >>= 4;
+                if (dst >= 0 && col < a.N) a.dbg[((int64_t)dst * a.N + col) * a.G + gg] = p;
+              }
+            }
+          }
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float pf = MG ? __int_as_float(part[nb][r]) : (float)part[nb][r];
+              acc[mb][nb][r] = __builtin_fmaf(pf, sv[nb], acc[mb][nb][r]);
+            }
+        };
+        i32x4 av[2][S];
+        i32x4 part[2][NB];
+        read_a(0, av[0]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          if (mb + 1 < MB) read_a(mb + 1, av[(mb + 1) & 1]);
+#pragma unroll
+          for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+              const i32x4 cin = (s == 0) ? (MG ? magic4 : i32x4{0, 0, 0, 0}) : part[mb & 1][nb];
+              part[mb & 1][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[mb & 1][s], bfr[nb][s], cin, 0, 0, 0);
+            }
+          if (mb > 0) fold(mb - 1, part[(mb - 1) & 1]);
+        }
+        fold(MB - 1, part[(MB - 1) & 1]);
+      }
+    }
+  };
+
+  // ---- main loop: chunk c uses ring slot c % RD ----------------------------
+  // 64/128-row tiles issue the next chunk's loads unconditionally, past the
+  // end with the chunk index clamped to the last chunk (loaded again, never
+  // used): no branch surrounds a load, so no join makes the compiler wait for
+  // one (which serialized their prefetch). The 16/32-row tiles run a few
+  // chunks per tile, where the extra chunk costs more than the join (measured
+  // on the decode points), so they skip the loads past the end.
+  constexpr bool CLAMP = BM >= 64;
+  const int last_chunk = c.nchunks - 1;
+  const int last_win = (c.nchunks + ZW - 1) / ZW - 1;
+  WChunk ring[RD];
+  // zs_cur serves the current window; zs_next is loaded one window ahead and
+  // copied in at each window start (after the activation wait, which has
+  // covered its load: it was issued before those activations)
+  ZsWin zs_cur, zs_next;
+  if constexpr (!ZS_LDS && ZSV) load_zs(0, zs_next);
+  load_x(0);
+#pragma unroll
+  for (int d = 0; d < RD - 1; ++d) {
+    if constexpr (CLAMP) {
+      load_w(min(d, last_chunk), ring[d]);
+    } else {
+      if (d < c.nchunks) load_w(d, ring[d]);
+    }
+  }
+  if constexpr (ZS_LDS) {
+    // visible to all waves after the first barrier of the loop; a symmetric
+    // tile stores its scales / 16 for the symmetric unpack (see compute)
+#pragma unroll
+    for (int j = 0; j < SU; ++j) {
+      const int u = tid + j * NT;
+      if (u < s_units) {
+        u32x4 v = sq[j];
+        if constexpr (MG) {
+          v.x = __float_as_uint(__uint_as_float(v.x) * 0.0625f);
+          v.y = __float_as_uint(__uint_as_float(v.y) * 0.0625f);
+          v.z = __float_as_uint(__uint_as_float(v.z) * 0.0625f);
+          v.w = __float_as_uint(__uint_as_float(v.w) * 0.0625f);
+        }
+        *reinterpret_cast<u32x4*>(s_scale + 4 * u) = v;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < ZU; ++j) {
+      const int u = tid + j * NT;
+      if (!MG && u < z_units) *reinterpret_cast<u32x4*>(s_zero + 16 * u) = zq[j];
+    }
+  }
+  // STAGGER (8-wave 256-column tiles): half of the waves run the chunk
+  // interval in the opposite order, so that the CU's load bursts and compute
+  // phases overlap: early waves loads(c+1), compute(c), store A(c+1); late
+  // waves compute(c), store A(c+1) (loaded one interval earlier), loads(c+2) --
+  // into the weight slot compute(c) has just finished with. One barrier per
+  // chunk for all waves, as in the plain loop. Waves are placed round-robin
+  // (w and w + 4 share a SIMD); of the groupings measured, late = waves 2, 3,
+  // 6, 7 (each SIMD's two waves in the same order, two SIMDs each way) was
+  // fastest -- faster than the SIMD mates in opposite orders. A wave raises
+  // its issue priority for its compute phase, so that a SIMD mate's loads and
+  // staging fill the gaps rather than delay the MFMA chain (measured -0.75 %
+  // over five interleaved runs).
+  constexpr bool STAGGER = NW == 8 && BMX == BM && RD == 2 && CLAMP;
+  if constexpr (STAGGER) {
+    // one interval of chunk cc (ring parity d); LATE selects the order
+    auto interval = [&](int cc, int d, auto late_tag) {
+      constexpr bool LATE = decltype(late_tag)::value;
+      if constexpr (!ZS_LDS && ZSV) {
+        if (d % ZW == 0) {
+          zs_cur = zs_next;
+          load_zs(min(cc / ZW + 1, last_win), zs_next);
+        }
+      }
+      if constexpr (LATE) {
+        __builtin_amdgcn_s_setprio(1);
+        compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
+        __builtin_amdgcn_s_setprio(0);
+        store_x((cc + 1) & 1);
+        load_x(min(cc + 2, last_chunk));
+        load_w(min(cc + 2, last_chunk), ring[d]);
+      } else {
+        load_x(min(cc + 1, last_chunk));
+        load_w(min(cc + 1, last_chunk), ring[(d + 1) % 2]);
+        __builtin_amdgcn_s_setprio(1);
+        compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
+        __builtin_amdgcn_s_setprio(0);
+        store_x((cc + 1) & 1);
+      }
+      __syncthreads();
+    };
+    // two separate loops (no join inside either, so no waits for loads there)
+    if (((tid >> 6) >> 1) & 1) {
+      // one more chunk in flight: A(1) in registers, W(1) in the ring
+      store_x(0);
+      load_x(min(1, last_chunk));
+      load_w(min(1, last_chunk), ring[1]);
+      __syncthreads();
+      for (int ch = 0; ch < c.nchunks; ch += 2) {
+        interval(ch, 0, std::true_type{});
+        if (ch + 1 < c.nchunks) interval(ch + 1, 1, std::true_type{});
+        rebase();
+      }
+    } else {
+      store_x(0);
+      __syncthreads();
+      for (int ch = 0; ch < c.nchunks; ch += 2) {
+        interval(ch, 0, std::false_type{});
+        if (ch + 1 < c.nchunks) interval(ch + 1, 1, std::false_type{});
+        rebase();
+      }
+    }
+  }
+  for (int ch = 0; ch < (STAGGER ? 0 : c.nchunks); ch += RD) {
+#pragma unroll
+    for (int d = 0; d < RD; ++d) {
+      const int cc = ch + d;
+      if (FAST || cc < c.nchunks) {
+        store_x(cc & 1);
+        __syncthreads();
+        if constexpr (!ZS_LDS && ZSV) {
+          if (d % ZW == 0) {
+            zs_cur = zs_next;
+            if (CLAMP || cc / ZW + 1 <= last_win) load_zs(min(cc / ZW + 1, last_win), zs_next);
+          }
+        }
+        if constexpr (CLAMP) {
+          load_x(min(cc + 1, last_chunk));
+          load_w(min(cc + RD - 1, last_chunk), ring[(d + RD - 1) % RD]);
+        } else {
+          if (cc + 1 < c.nchunks) load_x(cc + 1);
+          if (cc + RD - 1 < c.nchunks) load_w(cc + RD - 1, ring[(d + RD - 1) % RD]);
+        }
+        // the 8-wave kernel's half- and quarter-height bodies raise their
+        // priority for the compute phase as the staggered loop does (-0.8 %
+        // on DeepSeek-V3 up M=4096 over five interleaved runs); in the 4-wave
+        // 64-row kernel it measured 1-3 % slower
+        if constexpr (NW == 8) __builtin_amdgcn_s_setprio(1);
+        compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
+        if constexpr (NW == 8) __builtin_amdgcn_s_setprio(0);
+      }
+    }
+    rebase();
+  }
+
+  // (the reference-layout debug export passes no output)
+  if (!DEBUGP || a.out != nullptr) {
+    // 128-column tiles: the finished tile goes through LDS (the activation
+    // buffers are free now) so that every row leaves as 16-byte stores of
+    // its 256 contiguous bytes -- 8 store instructions per wave instead of 64
+    // two-byte ones (an MFMA lane holds four rows of one column). Row r's
+    // 16-byte segment s sits at r * 256 + 16 * (s ^ (r % 16)): the four rows
+    // of one ds_write_b16 hit distinct segments, and so do the two rows of a
+    // ds_read_b128 half-wave (opposite parity: disjoint bank halves).
+    constexpr bool TILE_OUT = (BN == 128 || BN == 256) && BM >= 64;
+    constexpr int SEG = BN / 8;          // 16-byte segments per tile row
+    constexpr int ROWB = BN * 2;         // bytes per tile row
+    bool stored = false;
+    if constexpr (TILE_OUT) {
+      if (a.vec_out) {
+        uint8_t* tile = reinterpret_cast<uint8_t*>(s_x);
+        __syncthreads();   // every wave has finished reading the activation buffers
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const int cl = c.col0 - c.tile_col0 + nb * 16 + jl;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int row = mb * 16 + kb * 4 + r;
+              v[r] = acc[mb][nb][r] * s_xs[row];
+              if constexpr (ROUTED) v[r] = v[r] * s_tw[row];
+            }
+            // rows r and r + 1 of the column converted as one pair
+            const uint32_t pk[2] = {bf16x2_rne(v[0], v[1]), bf16x2_rne(v[2], v[3])};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int row = mb * 16 + kb * 4 + r;
+              const int off = row * ROWB + (((cl >> 3) ^ (row & (SEG - 1))) << 4) + ((cl & 7) << 1);
+              *reinterpret_cast<uint16_t*>(tile + off) = (uint16_t)(pk[r >> 1] >> (16 * (r & 1)));
+            }
+          }
+        __syncthreads();
+        static_assert((BMX * SEG) % NT == 0, "output rounds");
+#pragma unroll
+        for (int i = 0; i < BMX * SEG / NT; ++i) {
+          const int t = tid + i * NT;
+          const int row = t / SEG, seg = t % SEG;
+          const u32x4 v = *reinterpret_cast<const u32x4*>(tile + row * ROWB + ((seg ^ (row & (SEG - 1))) << 4));
+          const int dst = s_dst[row];
+          const int col = c.tile_col0 + seg * 8;
+          if (dst >= 0 && col < a.N) *reinterpret_cast<u32x4*>(a.out + (int64_t)dst * a.ldo + col) = v;
+        }
+        stored = true;
+      }
+    }
+    if (!stored) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int col = c.col0 + nb * 16 + jl;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = mb * 16 + kb * 4 + r;
+            const int dst = s_dst[row];
+            if (dst >= 0 && col < a.N) {
+              float v = acc[mb][nb][r] * s_xs[row];
+              if constexpr (ROUTED) v = v * s_tw[row];
+              a.out[(int64_t)dst * a.ldo + col] = bf16_rne_bits(__float_as_uint(v));
+            }
+          }
+        }
+    }
+  }
+}
+
+// ZSG > 0: zero points and scales come from an LDS copy of the tile's
+// block; the host launches this only when G <= ZSG (see zs_block_fits).
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST, bool ZSV,
+          int WAVES_PER_EU>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU)))
+void w4a8_gemm_kernel(const GemmArgs a) {
+  constexpr int BN = NW * WN;
+  constexpr int PITCH = KCG * GS + 32;
+  constexpr bool ZS_LDS = ZSG > 0;
+  constexpr bool ROUTED = RMODE != 0;
+  static_assert(BM % 16 == 0 && WN % 16 == 0 && GS % 64 == 0, "tile shape");
+
+  __shared__ __attribute__((aligned(16))) int8_t s_x[2 * BM * PITCH];
+  __shared__ __attribute__((aligned(16))) float s_scale[ZS_LDS ? BN * ZSG : 4];
+  __shared__ __attribute__((aligned(16))) int8_t s_zero[ZS_LDS ? BN * ZSG : 16];
+  __shared__ int s_src[BM];
+  __shared__ int s_dst[BM];
+  __shared__ float s_xs[BM];
+  __shared__ float s_tw[BM];
+  __shared__ int s_rows;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // ---- tile decode -------------------------------------------------------
+  // The grid covers the worst-case block count; the actual count is only
+  // known here. Spread the actual tiles evenly over the 8 XCDs (workgroup L
+  // runs on XCD L % 8), each XCD taking a contiguous run of the tile list.
+  int nblocks;
+  if constexpr (ROUTED) {
+    // blocks past sorted_len / BM would read past sorted_ids / expert_ids
+    nblocks = min(a.num_post_pad[0] / BM, a.sorted_len / BM);
+  } else {
+    nblocks = a.blk_count[0];
+  }
+  // routed 64/128-row tiles may run in expert groups (the host decides)
+  const bool egroups = ROUTED && BM >= 64 && a.egroups;
+  const int span = a.n_tiles * a.R;
+  const int tiles = egroups ? nblocks * a.n_tiles : (nblocks + a.R - 1) / a.R * span;
+  const int per_xcd = (tiles + 7) >> 3;
+  const int L = blockIdx.x;
+  if ((L >> 3) >= per_xcd) return;
+  const int t = (L & 7) * per_xcd + (L >> 3);
+  if (t >= tiles) return;
+  int b, nt, e;
+  if (egroups) {
+    if (!expert_group_tile(t, a.n_tiles, a.R, nblocks, a.expert_ids, a.E, b, nt, e)) return;
+  } else {
+    const int chunk_id = t / span;
+    const int rem = t - chunk_id * span;
+    nt = rem / a.R;
+    b = chunk_id * a.R + (rem - nt * a.R);
+    if (b >= nblocks) return;
+    if constexpr (ROUTED) {
+      e = a.expert_ids[b];
+      if (e >= a.E) return;
+    } else {
+      e = a.blk_expert[b];
+    }
+    if (e < 0) return;
+  }
+
+  if (tid == 0) s_rows = 0;
+  __syncthreads();
+  // Tiles with an LDS zero/scale block: is every zero point of the tile's
+  // [BN x G] block 8 (symmetric int4)? The loads go out with the routing
+  // rows' and are checked at the same barrier. Columns past N read zero
+  // (not symmetric).
+  constexpr bool SYM_CHECK = ZSG > 0;
+  constexpr int ZCU = SYM_CHECK ? (BN * ZSG / 16 + NW * 64 - 1) / (NW * 64) : 1;
+  int zok = 1;
+  if constexpr (SYM_CHECK) {
+    const __amdgpu_buffer_rsrc_t zr = make_rsrc(a.wz + (int64_t)e * a.N * a.G, (uint32_t)(a.N * a.G));
+    const int z_units = BN * a.G / 16;
+#pragma unroll
+    for (int j = 0; j < ZCU; ++j) {
+      const int u = tid + j * NW * 64;
+      if (u < z_units) {
+        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(zr, (uint32_t)(nt * BN * a.G) + u * 16u, 0, 0);
+        zok &= (q.x == 0x08080808u) & (q.y == 0x08080808u) & (q.z == 0x08080808u) & (q.w == 0x08080808u);
+      }
+    }
+  }
+  if (tid < BM) {
+    int src = -1, dst = -1;
+    float xsv = 0.f, twv = 1.f;
+    if constexpr (ROUTED) {
+      const int s = a.sorted_ids[b * BM + tid];
+      if (s >= 0 && s < a.num_pairs) {
+        src = s / a.topk;
+        dst = s;
+        xsv = a.xs[src];
+        twv = a.tw ? a.tw[s] : 1.f;
+      }
+    } else {
+      const int r = a.blk_row0[b] + tid;
+      if (r < a.blk_row1[b]) {
+        src = dst = r;
+        if (!DEBUGP || a.xs != nullptr) xsv = a.xs[r];   // the debug export may pass no scales
+      }
+    }
+    s_src[tid] = src;
+    s_dst[tid] = dst;
+    s_xs[tid] = xsv;
+    s_tw[tid] = twv;
+    if (dst >= 0) atomicMax(&s_rows, tid + 1);
+  }
+  const bool tsym = SYM_CHECK ? __syncthreads_and(zok) != 0 : (__syncthreads(), false);
+  const int rows = __builtin_amdgcn_readfirstlane(s_rows);
+
+  TileCtx c;
+  c.e = e;
+  c.tile_col0 = nt * BN;
+  c.col0 = nt * BN + wave * WN;
+  c.nchunks = (a.G + KCG - 1) / KCG;
+  c.rows = rows;
+  // tiles whose valid rows fit in the top quarter (8-wave 128-row tiles: the
+  // second block of most DeepSeek-V3 experts) or half run a shorter body;
+  // symmetric tiles run the magic-number fold (SYMT)
+  auto run = [&](auto symt_c) {
+    constexpr bool SYMT = decltype(symt_c)::value;
+    if constexpr (BM >= 128 && NW == 8) {
+      if (rows <= BM / 4) {
+        gemm_body<BM / 4, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero,
+                                                                                    s_src, s_dst, s_xs, s_tw);
+        return;
+      }
+    }
+    if constexpr (BM >= 64) {
+      if (rows <= BM / 2) {
+        gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero,
+                                                                                    s_src, s_dst, s_xs, s_tw);
+        return;
+      }
+    }
+    gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero, s_src,
+                                                                            s_dst, s_xs, s_tw);
+  };
+  if constexpr (SYM_CHECK) {
+    if (tsym) run(std::true_type{});
+    else run(std::false_type{});
+  } else {
+    run(std::false_type{});
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launch geometry and dispatch.
+
+static void set_grid(GemmArgs& a, int max_blocks, int BN, int R) {
+  a.n_tiles = (a.N + BN - 1) / BN;
+  a.R = R;
+  const int chunks = (max_blocks + R - 1) / R;
+  a.total_tiles = chunks * R * a.n_tiles;
+  a.per_xcd = (a.total_tiles + 7) / 8;
+}
+
+// The tile's [BN x G] zero-point/scale block can be copied to an LDS array of
+// BN * ZSG entries in whole 16-byte units from 16-byte-aligned addresses.
+static bool zs_block_fits(const GemmArgs& a, int BN, int ZSG) {
+  return ZSG > 0 && a.G <= ZSG && (BN * a.G) % 16 == 0 && (a.N * a.G) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(a.wz) % 16 == 0 && (a.ws == nullptr || reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
+}
+
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, int WPE>
+static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
+  set_grid(a, max_blocks, NW * WN, R);
+  // a column's zero points / scales of one window can be read as one aligned
+  // run when G is a multiple of the window's groups and both tensors are
+  // 16-byte aligned
+  a.zs_vec = (a.G % (KCG * zs_window(KCG, RD)) == 0) && (reinterpret_cast<uintptr_t>(a.wz) % 16 == 0) &&
+             (reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
+  // output rows can be written in 16-byte pieces
+  a.vec_out = (a.N % 8 == 0) && (a.ldo % 8 == 0) && (reinterpret_cast<uintptr_t>(a.out) % 16 == 0);
+  // Expert groups pay a short search per tile; they pay off when an expert's
+  // weights outgrow one XCD's 4 MB L2 (below that the weights stay cached
+  // across row blocks anyway). Groups hold up to 4 blocks (set_grid has
+  // sized the grid for any grouping). Measured on MI355X: with 128-row tiles
+  // 4 beat 2, 8 and 16 on the skewed DeepSeek-V3 point; with 64-row tiles 4
+  // beat 2 by 2.5 % on DeepSeek-V3 down M=4096 (up to 3 blocks an expert).
+  a.egroups = RMODE != 0 && BM >= 64 && (int64_t)a.N * (a.K / 2) > (int64_t)4 << 20;
+  if (a.egroups) a.R = 4;
+  if (a.total_tiles == 0) return hipSuccess;
+  // the guard-free body needs whole chunks, a chunk count divisible by the
+  // unroll, and (without the LDS zero/scale block) aligned vector runs
+  constexpr bool CAN_FAST = BM <= 32;
+  constexpr bool RUNS = ZSG == 0;   // vector zero/scale runs apply
+  const dim3 grid(8 * a.per_xcd), block(NW * 64);
+  if (CAN_FAST && a.G % (KCG * RD) == 0 && (ZSG > 0 || a.zs_vec))
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, CAN_FAST, RUNS, WPE>), grid,
+                       block, 0, s, a);
+  else if (RUNS && a.zs_vec)
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, RUNS, WPE>), grid, block,
+                       0, s, a);
+  else
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, false, WPE>), grid, block,
+                       0, s, a);
+  return hipGetLastError();
+}
+
+// Row-block size -> tile body; instantiated per row source by the gemm_*.hip
+// files (declared in mw4a8_internal.h).
+template <int GS, int RMODE, bool DEBUGP>
+hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, hipStream_t s) {
+  constexpr int K512 = 512 / GS > 0 ? 512 / GS : 1;     // groups per 512 bytes of K
+  constexpr int K1024 = 1024 / GS > 0 ? 1024 / GS : 1;
+  constexpr int K256 = 256 / GS > 0 ? 256 / GS : 1;
+  switch (c.BM) {
+    case 16:
+      // 4-group chunks (at group size 128), two in flight per wave, two waves
+      // per SIMD: measured best or within 2 % on every decode point (M = 1
+      // to 64 of the DeepSeek-V3, Mixtral and Qwen3 shapes)
+      if (zs_block_fits(a, 64, 64)) return launch_one<16, 16, 4, GS, K512, 2, 64, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);
+      return launch_one<16, 16, 4, GS, K1024, 2, 0, RMODE, DEBUGP, 1>(a, max_blocks, c.R, s);
+    case 32:
+      if (zs_block_fits(a, 64, 64)) return launch_one<32, 16, 4, GS, K512, 2, 64, RMODE, DEBUGP, 1>(a, max_blocks, c.R, s);
+      return launch_one<32, 16, 4, GS, K512, 2, 0, RMODE, DEBUGP, 1>(a, max_blocks, c.R, s);
+    // three waves per SIMD fit the gs = 128 body without spills; the others keep two
+    case 64:
+      // G <= 16 (K <= 2048 at group size 128): the tile's [128 x G] zero/scale
+      // block in LDS (10 KB; three workgroups per CU still fit)
+      if (zs_block_fits(a, 128, 16))
+        return launch_one<64, 32, 4, GS, K256, 2, 16, RMODE, DEBUGP, GS == 128 ? 3 : 2>(a, max_blocks, c.R, s);
+      return launch_one<64, 32, 4, GS, K256, 2, 0, RMODE, DEBUGP, GS == 128 ? 3 : 2>(a, max_blocks, c.R, s);
+    case 128:
+      // group size 128: 8 waves x 32 columns, staggered (see STAGGER)
+      if constexpr (GS == 128) {
+        // the tile's whole [256 x G] zero-point/scale block in LDS when G <= 64
+        // (80 KB beside the 72 KB of activation buffers: one tile per CU)
+        if (zs_block_fits(a, 256, 64))
+          return launch_one<128, 32, 8, GS, K256, 2, 64, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);
+        return launch_one<128, 32, 8, GS, K256, 2, 0, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);
+      } else
+        return launch_one<128, 32, 4, GS, K256, 2, 0, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace mw4a8

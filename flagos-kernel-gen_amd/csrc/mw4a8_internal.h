@@ -49,8 +49,12 @@ struct GemmArgs {
 // the list and run at the same time on one XCD. Every block keeps n_tiles
 // tiles inside its group's range, so block t / n_tiles lies in the group of
 // tile t. Writes block b, column tile nt and expert e of tile t in
-// [0, nblocks * n_tiles); false when the block has no expert in [0, E) or the
-// blocks are out of order.
+// [0, nblocks * n_tiles); false when the block has no expert in [0, E).
+// The run start is found by a binary search, which needs ascending
+// expert_ids: on a table that is not sorted the returned group may not hold
+// block t / n_tiles, so every block of the group is checked to belong to e
+// -- a tile never computes a block with another expert's weights (its tiles
+// may then be skipped; the C ABI requires the ascending order).
 __host__ __device__ inline bool expert_group_tile(int t, int n_tiles, int R, int nblocks, const int32_t* expert_ids,
                                                   int E, int& b, int& nt, int& e) {
   const int bb = t / n_tiles;
@@ -63,6 +67,7 @@ __host__ __device__ inline bool expert_group_tile(int t, int n_tiles, int R, int
     else hi = mid;
   }
   const int g0 = lo + (bb - lo) / R * R;
+  if (expert_ids[g0] != e) return false;   // unsorted table
   int gs = 1;
   while (gs < R && g0 + gs < nblocks && expert_ids[g0 + gs] == e) ++gs;
   const int local = t - g0 * n_tiles;
@@ -70,6 +75,28 @@ __host__ __device__ inline bool expert_group_tile(int t, int n_tiles, int R, int
   b = g0 + (local - nt * gs);
   return nt < n_tiles;
 }
+
+// Scalar byte offset of K-group gg within a weight column (the vector part
+// of the address holds the column and the lane's 16-byte piece). Groups past
+// the last one -- loaded by a partial last K-chunk, never computed -- read
+// the last group again, so the offset stays inside the column: the buffer
+// range check does not cover scalar offsets.
+__host__ __device__ inline int w_group_soffset(int gg, int G, int GS) { return (gg < G ? gg : G - 1) * (GS / 2); }
+
+// Vector byte offset of a lane's weight pieces within one expert's
+// [N, K/2] slice: column col, K slot kb (0..3) of the MFMA operand, which
+// covers bytes kb * GS / 8 .. + GS / 8 of each group (16-byte pieces, or one
+// 8-byte piece at group size 64).
+__host__ __device__ inline uint32_t w_lane_offset(int col, uint32_t khalf, int kb, int GS) {
+  return (uint32_t)col * khalf + (uint32_t)(kb * (GS / 8));
+}
+
+// Tile bodies per group size, row source and debug export (gemm_kernel.h;
+// instantiated by the gemm_*.hip files).
+struct GemmArgs;
+struct TileConfig;
+template <int GS, int RMODE, bool DEBUGP>
+hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, hipStream_t s);
 
 struct TileConfig {
   int BM;     // rows per block
@@ -107,7 +134,10 @@ constexpr int kModeRoutedRepacked = 2;  // routed pairs, weights in the repacked
 hipError_t launch_grouped_gemm(GemmArgs a, const TileConfig& cfg, int group_size, int mode, int max_blocks,
                                hipStream_t s);
 
-hipError_t launch_debug_partials(GemmArgs a, int group_size, int max_blocks, hipStream_t s);
+// The same kernels with the debug export on: a.dbg [rows, N, G] receives
+// the exact int32 partial of every (row, column, group) the launch computes.
+hipError_t launch_debug_partials(GemmArgs a, const TileConfig& cfg, int group_size, int mode, int max_blocks,
+                                 hipStream_t s);
 
 // MoE-layer kernels around the GEMM (moe_layer.hip); shapes checked by the caller.
 hipError_t launch_quant_rows(const uint16_t* x, int64_t ldx, int M, int K, int8_t* q, int64_t ldq, float* scale,

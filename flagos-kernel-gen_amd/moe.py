@@ -34,11 +34,20 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def _capturing(device: torch.device) -> bool:
+    return torch.cuda.is_current_stream_capturing()
+
+
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Per-(device, stream) scratch buffer, grown on demand.
 
     Calls that share a stream are ordered, so they may share this buffer.
+    Under HIP-graph capture a fresh buffer is taken from the graph's memory
+    pool instead: the graph keeps its address, so a cached buffer that a
+    later eager call replaced (and freed) must never be one a graph uses.
     """
+    if _capturing(device):
+        return torch.empty(max(nbytes, 4096), dtype=torch.uint8, device=device)
     key = (device.index, _stream(device))
     buf = _WORKSPACES.get(key)
     if buf is None or buf.numel() < nbytes:
@@ -56,7 +65,11 @@ def _routing_buffer(device: torch.device, stream: int, n_int32: int) -> torch.Te
 
     A call's routing kernel writes it and the call's GEMM reads it; a later
     call on the same stream runs after both, so the calls may share it.
+    Under HIP-graph capture the call gets a fresh buffer from the graph's
+    pool (see ``_workspace``).
     """
+    if _capturing(device):
+        return torch.empty(max(n_int32, 1024), dtype=torch.int32, device=device)
     key = (device.index, stream)
     buf = _ROUTING.get(key)
     if buf is None or buf.numel() < n_int32:
@@ -172,6 +185,38 @@ def w4a8_group_partials(x_q, w_q4_packed, w_zero, expert_offsets, group_size):
     return out
 
 
+def w4a8_fused_moe_partials(x_q, x_scale, w_q4_packed, w_scale, w_zero, topk_ids, topk_weights,
+                            group_size: int = 128, block_m: int | None = None, weight_layout: str = "reference"):
+    """Debug export of the routed GEMM: runs the same kernel body as
+    ``w4a8_fused_moe`` and returns ``(out, partials)``, where ``partials
+    [M*topk, N, G]`` int32 holds the exact group partial sums of every routed
+    pair as its int32 MFMA chains computed them (zeros for unrouted pairs)."""
+    _need(weight_layout in ("reference", "mfma"), f"unknown weight_layout {weight_layout!r}")
+    M, K = x_q.shape
+    _check_activations(x_q, x_scale, M)
+    E, N, G = _check_weights(w_q4_packed, w_scale, w_zero, K, group_size)
+    _dtype(topk_ids, "topk_ids", torch.int32)
+    _dtype(topk_weights, "topk_weights", torch.float32)
+    topk = topk_ids.shape[1]
+    _need(topk_ids.is_contiguous() and tuple(topk_weights.shape) == (M, topk) and topk_weights.is_contiguous(),
+          "topk_ids / topk_weights must be contiguous [M, topk]")
+    dev = _on_gpu(dict(x_q=x_q, x_scale=x_scale, w_q4_packed=w_q4_packed, w_scale=w_scale, w_zero=w_zero,
+                       topk_ids=topk_ids, topk_weights=topk_weights))
+    P = M * topk
+    if block_m is None:
+        block_m = select_block_m(P, E, N, K, group_size)
+    sorted_ids, expert_ids, num_post, _ = moe_align_block_size(topk_ids, block_m, E)
+    out = torch.zeros(P, N, dtype=torch.bfloat16, device=dev)
+    partials = torch.zeros(P, N, G, dtype=torch.int32, device=dev)
+    rc = _lib.lib().mw4a8_debug_partials_routed(
+        _ptr(x_q), x_q.stride(0), _ptr(x_scale), _ptr(w_q4_packed), _ptr(w_scale), _ptr(w_zero),
+        _ptr(sorted_ids), _ptr(expert_ids), _ptr(num_post), _ptr(topk_weights), topk, _ptr(out), out.stride(0),
+        _ptr(partials), M, N, K, E, group_size, block_m, 1 if weight_layout == "mfma" else 0,
+        ctypes.c_void_p(_stream(dev)))
+    _lib.check(rc, "mw4a8_debug_partials_routed")
+    return out, partials
+
+
 def align_buffer_sizes(num_pairs: int, num_experts: int, block_m: int):
     sl, bl = ctypes.c_int(), ctypes.c_int()
     _lib.check(_lib.lib().mw4a8_align_sizes(num_pairs, num_experts, block_m, ctypes.byref(sl), ctypes.byref(bl)),
@@ -255,7 +300,8 @@ def w4a8_fused_moe(x_q: torch.Tensor, x_scale: torch.Tensor, w_q4_packed: torch.
         # internal routing metadata: carved from the stream's cached int32
         # buffer (no allocation per call)
         sl, bl = align_buffer_sizes(P, E, block_m)
-        base = _routing_buffer(dev, sid, sl + bl + 1).data_ptr()
+        rbuf = _routing_buffer(dev, sid, sl + bl + 1)   # held until both launches are enqueued
+        base = rbuf.data_ptr()
         sorted_p, expert_p, num_post_p = base, base + 4 * sl, base + 4 * (sl + bl)
         ids = topk_ids if topk_ids.is_contiguous() else topk_ids.contiguous()
         _lib.check(L.mw4a8_moe_align(_ptr(ids), P, E, block_m, sorted_p, expert_p, num_post_p, None, stream),

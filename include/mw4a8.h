@@ -114,6 +114,10 @@ int mw4a8_moe_align(const int32_t* topk_ids, int num_pairs, int E, int block_m, 
  *  sorted_ids / expert_ids / num_post_pad from mw4a8_moe_align with the
  *  same block_m, out [M * topk, N] bf16 (stride ldo). Rows of pairs that are
  *  not routed are left untouched. block_m in {16, 32, 64, 128}.
+ *  Routing metadata built by other means must have moe_align's form: each
+ *  expert's pairs in consecutive blocks and expert_ids non-decreasing over
+ *  the num_post_pad / block_m used blocks (blocks of an out-of-order table
+ *  may be skipped; none is computed with another expert's weights).
  */
 int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
                     const float* w_scale, const int8_t* w_zero, const int32_t* sorted_ids,
@@ -150,10 +154,29 @@ int mw4a8_fused_moe_repacked(const int8_t* x_q, int64_t ldx, const float* x_scal
  * (reference docs/Task1.md:99-104, the "mgk,ngk->mng" einsum) for the
  * rows owned by some expert; other rows are left untouched.
  * partials: [M_total, N, K/group_size] int32. Workspace as mw4a8_grouped_gemm.
+ * Runs the kernel body mw4a8_grouped_gemm selects for the same problem
+ * (same tile, same unpack and accumulation chains); each partial is read
+ * from its int32 MFMA chain.
  */
 int mw4a8_debug_partials(const int8_t* x_q, int64_t ldx, const uint8_t* w_q4, const int8_t* w_zero,
                          const int32_t* expert_offsets, int32_t* partials, int M_total, int N, int K,
                          int E, int group_size, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Routed debug export (no reference counterpart): mw4a8_fused_moe (repacked
+ * != 0: mw4a8_fused_moe_repacked) with the same arguments and the same kernel
+ * body -- out is written as by that call -- that also writes the exact int32
+ * group partials of every routed pair i = m * topk + j:
+ *   partials[i, n, g] = sum_{k in g} x_q[m,k] * int8(nib(w[e,n,k]) - zero[e,n,g])
+ * partials: [M * topk, N, K/group_size] int32 (rows of unrouted pairs untouched).
+ * On symmetric tiles the body's chains hold 16x the partial, seeded with the
+ * float bits of 1.5 * 2^23; the export undoes both exactly.
+ */
+int mw4a8_debug_partials_routed(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
+                                const float* w_scale, const int8_t* w_zero, const int32_t* sorted_ids,
+                                const int32_t* expert_ids, const int32_t* num_post_pad, const float* topk_weights,
+                                int topk, uint16_t* out_bf16, int64_t ldo, int32_t* partials, int M, int N, int K,
+                                int E, int group_size, int block_m, int repacked, void* stream);
 
 /*
  * ---- MoE-layer kernels around the GEMM -------------------------------------
