@@ -20,6 +20,7 @@ SIGNATURES = {
     "mw4a8_abi_version": (_i, []),
     "mw4a8_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "mw4a8_grouped_gemm": (_i, [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i, _i, _i, _i, _i, _p, _sz, _p]),
+    "mw4a8_grouped_gemm_noalloc": (_i, [_p, _i64, _p, _p, _p, _p, _p, _p, _i64, _i, _i, _i, _i, _i, _p]),
     "mw4a8_align_sizes": (_i, [_i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "mw4a8_select_block_m": (_i, [_i, _i, _i, _i, _i]),
     "mw4a8_moe_align": (_i, [_p, _i, _i, _i, _p, _p, _p, _p, _p]),

@@ -4,6 +4,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/mw4a8.h"
 #include "mw4a8_internal.h"
 #include "mw4a8_pack.h"
@@ -126,6 +128,51 @@ int run_csr(GemmArgs a, const int32_t* offsets, int M_total, int E, int gs, void
   return MW4A8_OK;
 }
 
+// ---- allocation-free variant of the reference-layout entry ----------------
+// mw4a8_grouped_gemm_noalloc keeps its block table (the only device memory
+// the reference-layout entry needs beyond inputs and outputs) in `scratch`,
+// a file-scope device array: one copy per GPU, held until the process ends,
+// sized for kNoallocMaxBlocks row blocks. Host code never passes the array's
+// name to a kernel (on the host it is a stand-in, not a device address): the
+// first call on a device resolves the device's own address of the array with
+// hipGetSymbolAddress, with that device current, and keeps it per device.
+// The block-table kernel writes every entry the GEMM reads, so nothing has
+// to be cleared between calls.
+constexpr int kNoallocMaxBlocks = 65536;
+constexpr size_t kNoallocScratchBytes = 256 + 3 * sizeof(int32_t) * (size_t)kNoallocMaxBlocks;   // 786688
+static_assert(kNoallocScratchBytes % 256 == 0, "scratch is whole 256-byte units");
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) uint8_t scratch[kNoallocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// This device's address of `scratch` (resolved once per device); the stream
+// must belong to the current device.
+int noalloc_scratch(hipStream_t s, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(MW4A8_ERR_UNSUPPORTED, "device %d beyond %d", dev, kMaxDevices);
+  if (s != nullptr) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(s, &sdev);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamGetDevice");
+    if (sdev != dev) return fail(MW4A8_ERR_INVALID, "stream is on device %d, current device is %d", (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (ptr == nullptr || !aligned(ptr, 256)) return fail(MW4A8_ERR_HIP, "unusable scratch address %p", ptr);
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MW4A8_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -153,6 +200,31 @@ int mw4a8_grouped_gemm(const int8_t* x_q, int64_t ldx, const float* x_scale, con
   if (rc) return rc;
   GemmArgs a = base_args(x_q, ldx, M_total, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, N, K, group_size);
   return run_csr(a, expert_offsets, M_total, E, group_size, workspace, ws_bytes,
+                 static_cast<hipStream_t>(stream), false);
+}
+
+int mw4a8_grouped_gemm_noalloc(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
+                               const float* w_scale, const int8_t* w_zero, const int32_t* expert_offsets,
+                               uint16_t* out_bf16, int64_t ldo, int M_total, int N, int K, int E, int group_size,
+                               void* stream) {
+  g_err[0] = 0;
+  if (M_total == 0) return MW4A8_OK;
+  int rc = check_gemm_args(x_q, ldx, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, M_total, N, K, E,
+                           group_size, true);
+  if (rc) return rc;
+  // the block table of the tile mw4a8_grouped_gemm would select must fit
+  const int ne = E < M_total ? E : M_total;
+  const int max_blocks = max_row_blocks(M_total, E, select_tiles(M_total, ne, N, K, group_size).BM);
+  if (csr_ws_bytes(max_blocks) > kNoallocScratchBytes)
+    return fail(MW4A8_ERR_UNSUPPORTED,
+                "mw4a8_grouped_gemm_noalloc: up to %d row blocks exceed its fixed scratch of %d blocks "
+                "(%zu bytes); use mw4a8_grouped_gemm with a workspace",
+                max_blocks, kNoallocMaxBlocks, kNoallocScratchBytes);
+  void* ws = nullptr;
+  rc = noalloc_scratch(static_cast<hipStream_t>(stream), &ws);
+  if (rc) return rc;
+  GemmArgs a = base_args(x_q, ldx, M_total, x_scale, w_q4, w_scale, w_zero, out_bf16, ldo, N, K, group_size);
+  return run_csr(a, expert_offsets, M_total, E, group_size, ws, kNoallocScratchBytes,
                  static_cast<hipStream_t>(stream), false);
 }
 

@@ -74,6 +74,24 @@ int mw4a8_grouped_gemm(const int8_t* x_q, int64_t ldx, const float* x_scale, con
                        void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * mw4a8_grouped_gemm without a workspace: allocates nothing and takes no
+ * workspace argument. No counterpart in the reference; for callers that
+ * cannot allocate device memory (code under HIP-graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments, kernels and
+ * results as mw4a8_grouped_gemm; its per-call block table lives in a fixed
+ * device array of the library (786688 bytes per GPU, held until the process
+ * ends) that bounds a call to 65536 row blocks -- about 65536 rows (fewer
+ * when experts end in partial blocks); larger calls return
+ * MW4A8_ERR_UNSUPPORTED. The stream must belong to the current device. Every
+ * call on one GPU shares that array: calls that overlap on one GPU (e.g. on
+ * two streams at once) race and must be ordered by the caller.
+ */
+int mw4a8_grouped_gemm_noalloc(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
+                               const float* w_scale, const int8_t* w_zero, const int32_t* expert_offsets,
+                               uint16_t* out_bf16, int64_t ldo, int M_total, int N, int K, int E, int group_size,
+                               void* stream);
+
+/*
  * Lengths of the routing buffers for num_pairs = M * topk pairs:
  *  *sorted_len = num_pairs + E * (block_m - 1), *blocks_len = ceil(sorted_len / block_m).
  * No reference counterpart (the reference receives pre-grouped rows).

@@ -42,6 +42,9 @@ int main() {
   expect(mw4a8_grouped_gemm(x, 1 << 20, f, w, f, z, o, out, 64, 4096, 64, 256, 2, 128, p, 1 << 20, NULL), -2,
          "32-bit offsets");
   expect(mw4a8_debug_partials(x, 256, w, z, o, i32, 4, 64, 200, 2, 128, p, 1 << 20, NULL), -1, "debug K % gs");
+  expect(mw4a8_grouped_gemm_noalloc(x, 256, f, w, f, z, o, out, 64, 800000, 64, 256, 100000, 128, NULL), -2,
+         "noalloc beyond its scratch");
+  expect(mw4a8_grouped_gemm_noalloc(x, 260, f, w, f, z, o, out, 64, 4, 64, 256, 2, 128, NULL), -1, "noalloc ldx");
   // routing and the routed GEMM
   expect(mw4a8_moe_align(o, 8, 2048, 16, i32, i32, i32, NULL, NULL), -2, "E > 1024");
   expect(mw4a8_moe_align(NULL, 8, 8, 16, i32, i32, i32, NULL, NULL), -1, "null ids");

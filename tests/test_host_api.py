@@ -84,6 +84,14 @@ def test_c_abi_rejects_bad_arguments_without_device_work(pkg):
     assert rc == -2
     # zero rows is a no-op
     assert L.mw4a8_grouped_gemm(p, 256, p, p, p, p, p, p, 64, 0, 64, 256, 2, 128, p, 1 << 20, None) == 0
+    # the allocation-free entry: same argument checks; a call whose block table
+    # exceeds its fixed scratch (800000 rows over 100000 experts: up to 143750
+    # 16-row blocks > 65536) is refused before any device work
+    rc = L.mw4a8_grouped_gemm_noalloc(p, 256, p, p, p, p, p, p, 64, 4, 64, 200, 2, 128, None)
+    assert rc == -1 and "multiple" in _lib.last_error()
+    rc = L.mw4a8_grouped_gemm_noalloc(p, 256, p, p, p, p, p, p, 64, 800000, 64, 256, 100000, 128, None)
+    assert rc == -2 and "scratch" in _lib.last_error()
+    assert L.mw4a8_grouped_gemm_noalloc(p, 256, p, p, p, p, p, p, 64, 0, 64, 256, 2, 128, None) == 0
 
 
 def test_layer_entries_reject_bad_arguments_without_device_work(pkg):
