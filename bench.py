@@ -6,13 +6,17 @@ K=7168, N=4096, int4 group 128), M=4096 tokens. One step is one routed call
 
 The JSON line carries ``value`` = microseconds per step, the GEMM kernel's
 roofline (algorithmic bytes and int8 ops per launch divided by its average
-duration from HIP events on the launch stream), the other DeepSeek-V3 points
-(decode M=1/64, down projection) as ``points``, and the CPU baseline: the
-oracle restatement of the reference operator timed on a bounded sample of
-the same workload on the host cores, scaled to one call.
+duration from HIP events on the launch stream, >= 50 launches, mean and
+median), every other configuration point as ``points`` (decode points with
+the rate of a plain cold read of the same byte count beside them), the
+drop-in reference-layout operator on the reference's ten workloads as
+``dropin`` (with the CPU oracle on the same inputs), two DeepSeek-V3 MoE
+layers as ``layers``, and the CPU baseline: the oracle restatement of the
+reference operator timed on a bounded sample of the headline workload on the
+host cores, scaled to one call.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--points all|none|name:M,...]
-                       [--no-cpu] [--cpu-seconds S]
+                       [--no-cpu] [--cpu-seconds S] [--no-dropin] [--no-layer]
 """
 
 from __future__ import annotations
@@ -30,11 +34,16 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA
 HEADLINE = ("dsv3_up", 4096)
-DEFAULT_POINTS = ("dsv3_up:1", "dsv3_up:64", "dsv3_down:1", "dsv3_down:64", "dsv3_down:4096")
 ALL_POINTS = ("tiny:64", "mixtral_up:1", "mixtral_up:8", "mixtral_up:32", "qwen3_up:16", "qwen3_up:256",
               "qwen3_up:2048", "dsv3_up:1", "dsv3_up:64", "dsv3_down:1", "dsv3_down:64", "dsv3_down:4096",
               "dsv3_skew:4096")
+DEFAULT_POINTS = ALL_POINTS
+# decode points (HBM-bound, judged against the >= 70 % of HBM target): each
+# also gets the measured rate of a plain cold read of the same byte count
+DECODE_POINTS = ("mixtral_up:1", "mixtral_up:8", "mixtral_up:32", "qwen3_up:16", "dsv3_up:1", "dsv3_up:64",
+                 "dsv3_down:1", "dsv3_down:64")
 ROTATE_BYTES = 1 << 30       # keep > 4x the 256 MB Infinity Cache in rotation
+MIN_EVENTS = 50              # HIP-event samples per kernel timing (median of >= 50)
 
 
 def log(msg):
@@ -149,26 +158,157 @@ def prime(fn, min_ms=100.0):
     torch.cuda.synchronize()
 
 
-def measure_point(pt, steps, warmup):
+def cold_read_ceiling(pkg, nbytes, dev, steps, warmup):
+    """Memory ceiling of a point: the HBM rate of moving ``nbytes`` cold, by
+    two plain streaming kernels over equally sized buffers rotated through
+    more than ``ROTATE_BYTES`` (each pass misses the 256 MB Infinity Cache):
+
+    * ``stream``: the library's measurement kernel ``mw4a8_stream_read``
+      (coalesced 16-byte loads, eight in flight per thread), the better of a
+      2048- and a 256-workgroup grid;
+    * ``torch_copy``: ``Tensor.copy_`` of ``nbytes / 2`` (reads and writes
+      ``nbytes`` in all) -- the fastest plain torch op on this box (its
+      reductions stay below 4 TB/s).
+
+    Returns a dict of GB/s (median of the HIP-event timings) per method."""
+    import ctypes
     import torch
+    from flagos_kernel_gen_amd import _lib
+    L = _lib.lib()
+    n16 = max(1, nbytes // 16)
+    nbuf = max(2, min(64, -(-ROTATE_BYTES // (16 * n16)) + 1))
+    bufs = [torch.empty(16 * n16, dtype=torch.uint8, device=dev) for _ in range(nbuf)]
+    sink = torch.zeros(4096, dtype=torch.uint8, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    out = {}
+    best = None
+    for blocks in (2048, 256):
+        def read(i, blocks=blocks):
+            _lib.check(L.mw4a8_stream_read(ctypes.c_void_p(bufs[i % nbuf].data_ptr()), 16 * n16,
+                                           ctypes.c_void_p(sink.data_ptr()), 4096, blocks, stream),
+                       "mw4a8_stream_read")
+        prime(read, 20.0)
+        _, med_us = kernel_events(read, steps, warmup)
+        gbs = 16 * n16 / (med_us * 1e-6) / 1e9
+        best = gbs if best is None else max(best, gbs)
+    out["stream"] = round(best, 1)
+    half = [b[: 8 * n16] for b in bufs]
+    dst = torch.empty(8 * n16, dtype=torch.uint8, device=dev)
+
+    def copy(i):
+        dst.copy_(half[i % nbuf])
+
+    prime(copy, 20.0)
+    _, med_us = kernel_events(copy, steps, warmup)
+    out["torch_copy"] = round(16 * n16 / (med_us * 1e-6) / 1e9, 1)
+    del bufs, half, dst
+    torch.cuda.empty_cache()
+    return out
+
+
+def measure_point(pt, steps, warmup, ceiling=False):
+    """Routed call (host clock over ``steps`` calls) and GEMM kernel (HIP
+    events over at least ``MIN_EVENTS`` launches: mean and median). With
+    ``ceiling`` the point also reports the rate of a plain cold read of its
+    algorithmic byte count (``cold_read_ceiling``) and the GEMM's fraction of
+    it."""
     prime(pt.step)
     us_step = time_steps(pt.step, steps, warmup) * 1e6
-    us_gemm, us_gemm_med = kernel_events(pt.gemm, steps, warmup)
+    n_ev = max(steps, MIN_EVENTS)
+    us_gemm, us_gemm_med = kernel_events(pt.gemm, n_ev, warmup)
     n = pt.n_sets
-    bytes_ = statistics.mean(pt.alg[i % n]["bytes"] for i in range(steps))
+    bytes_ = statistics.mean(pt.alg[i % n]["bytes"] for i in range(n_ev))
     ops = pt.alg[0]["ops"]
     gbs = bytes_ / (us_gemm * 1e-6) / 1e9
+    gbs_med = bytes_ / (us_gemm_med * 1e-6) / 1e9
     tops = ops / (us_gemm * 1e-6) / 1e12
-    del torch
-    return {
+    res = {
         "workload": f"{pt.shape.name}:M={pt.M}", "E": pt.shape.E, "topk": pt.shape.topk, "K": pt.shape.K,
         "N": pt.shape.N, "block_m": pt.block_m, "us_per_call": round(us_step, 2),
-        "gemm_us": round(us_gemm, 2), "gemm_us_median": round(us_gemm_med, 2),
+        "gemm_us": round(us_gemm, 2), "gemm_us_median": round(us_gemm_med, 2), "gemm_events": n_ev,
         "touched_experts": pt.alg[0]["touched_experts"], "alg_bytes": int(bytes_), "alg_ops": int(ops),
         "gemm_GBps": round(gbs, 1), "gemm_TOPS": round(tops, 2),
-        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "hbm_frac_median": round(gbs_med / HBM_PEAK_GBS, 4),
+        "mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
         "weight_sets": len(pt.inputs), "routing_sets": len(pt.routings),
     }
+    if ceiling:
+        ceil = cold_read_ceiling(pt.pkg, int(bytes_), pt.dev, n_ev, warmup)
+        top = max(ceil.values())
+        res["ceiling_GBps"] = ceil
+        res["gemm_over_ceiling_median"] = round(gbs_med / top, 4)
+    return res
+
+
+def dropin_algorithmic(E, M, N, K, gs, offsets):
+    """Bytes and int8 ops of one reference-layout call: the weights of every
+    expert that owns rows, the activation rows with their scales, the CSR
+    offsets and the bf16 output rows."""
+    G = K // gs
+    offs = [min(max(int(v), 0), M) for v in offsets.tolist()]
+    rows = [max(0, b - a) for a, b in zip(offs[:-1], offs[1:])]
+    touched = sum(1 for r in rows if r > 0)
+    covered = sum(rows)
+    nbytes = touched * (N * K // 2 + 4 * N * G + N * G) + covered * K + 4 * covered + 4 * (E + 1) + 2 * covered * N
+    return {"touched_experts": touched, "rows": covered, "bytes": nbytes, "ops": 2 * covered * N * K}
+
+
+def measure_dropin(pkg, dev, steps, warmup, cpu=True):
+    """The drop-in entry ``w4a8_group_gemm_moe`` on the reference's ten
+    workloads (docs/Task1.md:30-41): µs per operator call (HIP events around
+    the call: block-table kernel + GEMM; weight copies rotated so every call
+    reads cold HBM), algorithmic GB/s and TOPS, and the CPU oracle on the
+    same inputs (the reference's own all-expert unpack, docs/Task1.md:78-85)
+    on the host cores."""
+    import torch
+    from oracle import task1_ref
+    wl = pkg.workloads
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    results = []
+    for idx, (E, M, N, K, gs) in enumerate(wl.TASK1_WORKLOADS):
+        x_q, x_scale, w_q4, w_scale, w_zero, offs = wl.make_grouped_inputs(E, M, N, K, gs, seed=idx)
+        alg = dropin_algorithmic(E, M, N, K, gs, offs)
+        g_in = [t.to(dev) for t in (x_q, x_scale, offs)]
+        wbytes = w_q4.numel() + 5 * w_zero.numel()
+        ncopies = max(1, min(16, -(-ROTATE_BYTES // wbytes)))
+        sets = [tuple(t.to(dev) for t in (w_q4, w_scale, w_zero))]
+        for c in range(1, ncopies):
+            sets.append(wl.make_weights(E, N, K, gs, seed=4000 + 17 * c + idx, device=dev))
+        out = torch.zeros(M, N, dtype=torch.bfloat16, device=dev)
+
+        def call(i):
+            w = sets[i % len(sets)]
+            pkg.w4a8_group_gemm_moe(g_in[0], g_in[1], w[0], w[1], w[2], g_in[2], out, gs)
+
+        prime(call, 30.0)
+        n_ev = max(steps, MIN_EVENTS)
+        us, us_med = kernel_events(call, n_ev, warmup)
+        res = {"workload": f"task1[{idx}]", "E": E, "M_total": M, "N": N, "K": K, "group_size": gs,
+               "op_us": round(us, 2), "op_us_median": round(us_med, 2), "events": n_ev,
+               "weight_sets": len(sets), "touched_experts": alg["touched_experts"], "alg_bytes": alg["bytes"],
+               "GBps": round(alg["bytes"] / (us * 1e-6) / 1e9, 1),
+               "hbm_frac": round(alg["bytes"] / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+               "TOPS": round(alg["ops"] / (us * 1e-6) / 1e12, 3),
+               "mfma_frac": round(alg["ops"] / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 5)}
+        del sets, out, g_in
+        torch.cuda.empty_cache()
+        if cpu:
+            ref_out = torch.zeros(M, N, dtype=torch.bfloat16)
+            ts = []
+            for rep in range(4):
+                t0 = time.perf_counter()
+                task1_ref.w4a8_group_gemm_moe_ref(x_q, x_scale, w_q4, w_scale, w_zero, offs, ref_out, gs,
+                                                  unpack="all")
+                ts.append(time.perf_counter() - t0)
+                if sum(ts) > 3.0:
+                    break
+            cpu_us = statistics.median(ts[1:] if len(ts) > 1 else ts) * 1e6
+            res.update({"cpu_us": round(cpu_us, 1), "cpu_cores": cores, "cpu_runs": len(ts),
+                        "gpu_speedup_vs_cpu": round(cpu_us / us, 1)})
+        results.append(res)
+        log(json.dumps(res))
+    return results
 
 
 LAYER_POINTS = ("dsv3_layer:64", "dsv3_layer:4096")
@@ -300,6 +440,10 @@ def main():
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE against known bytes")
     ap.add_argument("--workload", default=None,
                     help="name:M to measure instead of the headline (profiling); implies --headline-only")
+    ap.add_argument("--no-dropin", action="store_true",
+                    help="skip the reference-layout drop-in on the reference's ten workloads")
+    ap.add_argument("--dropin-only", action="store_true",
+                    help="measure only the drop-in workloads (profiling; prints their JSON, not the bench line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -314,6 +458,10 @@ def main():
     if args.layer_only:
         layers = [measure_layer(pkg, int(m), dev, args.steps, args.warmup) for m in args.layers.split(",")]
         print(json.dumps({"layers": layers}), flush=True)
+        return
+    if args.dropin_only:
+        print(json.dumps({"dropin": measure_dropin(pkg, dev, args.steps, args.warmup, cpu=not args.no_cpu)}),
+              flush=True)
         return
 
     head_name, head_m = HEADLINE
@@ -331,7 +479,7 @@ def main():
         for inp in hp.inputs:
             inp.w_q4 = pkg.repack_weights(inp.w_q4)
         hp.weight_layout = "mfma"
-        us_m, med_m = kernel_events(hp.gemm, args.steps, args.warmup)
+        us_m, med_m = kernel_events(hp.gemm, max(args.steps, MIN_EVENTS), args.warmup)
         head_mfma = {"workload": head["workload"], "weight_layout": "mfma", "gemm_us": round(us_m, 2),
                      "gemm_us_median": round(med_m, 2),
                      "gemm_GBps": round(head["alg_bytes"] / (us_m * 1e-6) / 1e9, 1),
@@ -347,11 +495,17 @@ def main():
             name, M = item.split(":")
             log(f"point {name} M={M}")
             pt = Point(pkg, name, int(M), dev)
-            # side points: at least 10 warm-up and 50 timed calls (mean and median)
-            points.append(measure_point(pt, max(args.steps, 50), max(args.warmup, 10)))
+            # side points: at least 10 warm-up and 50 timed calls (mean and median);
+            # decode points also measure the cold-read ceiling of their byte count
+            points.append(measure_point(pt, max(args.steps, 50), max(args.warmup, 10), ceiling=item in DECODE_POINTS))
             log(json.dumps(points[-1]))
             del pt
             torch.cuda.empty_cache()
+
+    dropin = []
+    if not args.headline_only and not args.no_dropin:
+        log("drop-in w4a8_group_gemm_moe on the reference's ten workloads")
+        dropin = measure_dropin(pkg, dev, args.steps, max(args.warmup, 10), cpu=not args.no_cpu)
 
     layers = []
     if not args.headline_only and not args.no_layer:
@@ -401,6 +555,7 @@ def main():
         "headline": head,
         "headline_mfma_layout": head_mfma,
         "points": points,
+        "dropin": dropin,
         "layers": layers,
     }
     print(json.dumps(line), flush=True)

@@ -36,6 +36,7 @@ SIGNATURES = {
     "mw4a8_router_topk": (_i, [_p, _i64, _i, _i, _i, _i, _p, _p, _p]),
     "mw4a8_silu_mul_quant": (_i, [_p, _i64, _i, _i, _p, _i64, _p, _p]),
     "mw4a8_combine_topk": (_i, [_p, _i64, _i, _i, _i, _p, _p, _i64, _p]),
+    "mw4a8_stream_read": (_i, [_p, _i64, _p, _sz, _i, _p]),
     "mw4a8_host_selftest": (_i, []),
 }
 

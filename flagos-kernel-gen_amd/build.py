@@ -23,7 +23,8 @@ ARCH = "gfx950"
 # the grouped GEMM's kernel template (gemm_kernel.h) is instantiated per row
 # source in the gemm_*.hip files, which compile in parallel
 SOURCES = ("gemm_routed.hip", "gemm_csr.hip", "gemm_repacked.hip", "gemm_debug_routed.hip", "gemm_debug_csr.hip",
-           "gemm_debug_repacked.hip", "api.hip", "moe_align.hip", "grouped_gemm.hip", "moe_layer.hip")
+           "gemm_debug_repacked.hip", "api.hip", "moe_align.hip", "grouped_gemm.hip", "moe_layer.hip",
+           "measure.hip")
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -438,6 +438,20 @@ int mw4a8_combine_topk(const uint16_t* y_bf16, int64_t ldy, int M, int topk, int
   return MW4A8_OK;
 }
 
+int mw4a8_stream_read(const void* src, int64_t bytes, void* sink, size_t sink_bytes, int blocks, void* stream) {
+  g_err[0] = 0;
+  if (bytes < 0 || bytes % 16 != 0) return fail(MW4A8_ERR_INVALID, "bytes=%lld must be a non-negative multiple of 16",
+                                                (long long)bytes);
+  if (blocks < 1 || blocks > 65536) return fail(MW4A8_ERR_INVALID, "blocks=%d not in [1, 65536]", blocks);
+  if (!sink || sink_bytes < 4096 || !aligned(sink, 16))
+    return fail(MW4A8_ERR_INVALID, "sink must be a 16-byte aligned buffer of at least 4096 bytes");
+  if (bytes == 0) return MW4A8_OK;
+  if (!src || !aligned(src, 16)) return fail(MW4A8_ERR_INVALID, "src must be a 16-byte aligned device pointer");
+  hipError_t e = launch_stream_read(src, bytes, sink, blocks, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "stream_read launch");
+  return MW4A8_OK;
+}
+
 // ---------------------------------------------------------------------------
 
 int mw4a8_host_selftest(void) {

@@ -181,16 +181,47 @@ __device__ __forceinline__ int unit_pos(int cu) {
 // Chunks per zero-point/scale window (ZSV): the window's runs are read with
 // one vector load each per column block. RD chunks (the loop's unroll) while
 // the window's scales fit in 8 registers, else one chunk.
-__host__ __device__ constexpr int zs_window(int kcg, int rd) { return kcg * rd <= 8 ? rd : 1; }
+// Decode tiles (bm < 64) keep one chunk per window: each ring slot carries
+// its chunk's runs, requested with the chunk's weights.
+__host__ __device__ constexpr int zs_window(int kcg, int rd, int bm) { return bm < 64 ? 1 : (kcg * rd <= 8 ? rd : 1); }
 
 // Per-tile values shared by the kernel's setup and its tile bodies.
 struct TileCtx {
   int e;          // expert
+  int blk;        // row block
   int col0;       // first column of this wave
   int tile_col0;  // first column of the workgroup's tile
   int nchunks;    // K-chunks
   int rows;       // rows of the tile holding data (the rest is padding)
 };
+
+// Row r of row block b: the activation row it reads (src) and the output
+// row it writes (dst), -1 for padding. Routed: the pair in slot b * BM + r
+// of sorted_ids; reference layout: row blk_row0[b] + r below blk_row1[b].
+template <int BM, bool ROUTED>
+__device__ __forceinline__ void row_source(const GemmArgs& a, int b, int r, int& src, int& dst) {
+  src = dst = -1;
+  if constexpr (ROUTED) {
+    const int s = a.sorted_ids[b * BM + r];
+    if (s >= 0 && s < a.num_pairs) {
+      src = s / a.topk;
+      dst = s;
+    }
+  } else {
+    const int row = a.blk_row0[b] + r;
+    if (row < a.blk_row1[b]) src = dst = row;
+  }
+}
+
+// Epilogue factors of a row with dst >= 0: activation scale and (routed)
+// top-k weight. The reference-layout debug export may pass no scales.
+template <bool ROUTED, bool DEBUGP>
+__device__ __forceinline__ void row_scales(const GemmArgs& a, int src, int dst, float& xsv, float& twv) {
+  xsv = 0.f;
+  twv = 1.f;
+  if (!DEBUGP || a.xs != nullptr) xsv = a.xs[src];
+  if constexpr (ROUTED) twv = a.tw ? a.tw[dst] : 1.f;
+}
 
 // Main K loop and epilogue for the first BMX rows of a tile (BMX <= BM).
 //
@@ -207,7 +238,7 @@ struct TileCtx {
 //     (Used for the 16- and 32-row tiles only: without the guards the
 //     compiler schedules the larger bodies into scratch.)
 // ZSV (ZSG == 0 only): the zero points and scales of a window of
-//     zs_window(KCG, RD) chunks are read as one aligned vector run each per
+//     zs_window(KCG, RD, BM) chunks are read as one aligned vector run each per
 //     column (host-checked: G a multiple of the window's groups, 16-byte
 //     aligned tensors); otherwise one scalar load per group and chunk. Every
 //     such load costs the memory pipeline about as much as a 1 KB weight
@@ -220,8 +251,7 @@ struct TileCtx {
 template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST,
           bool ZSV, bool SYMT>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, int8_t* s_x, float* s_scale,
-                                          int8_t* s_zero, const int* s_src, const int* s_dst, const float* s_xs,
-                                          const float* s_tw) {
+                                          int8_t* s_zero, int* s_src, int* s_dst, float* s_xs, float* s_tw) {
   constexpr int NT = NW * 64;
   constexpr int MB = BMX / 16;        // 16-row blocks computed
   constexpr int NB = WN / 16;         // 16-column blocks per wave
@@ -249,6 +279,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   const int kb = lane >> 4;   // K slot group of the MFMA operands
   const uint32_t khalf = (uint32_t)a.K / 2;
 
+  // Decode tiles (XDEEP, defined below with the activation ring) read their
+  // routing rows here, before any weight load: loads complete in issue order,
+  // so waiting for these rows never waits for the weights requested next.
+  int r_src = -1, r_dst = -1;
+  if constexpr (BM < 64) {
+    if (tid < BM) row_source<BM, ROUTED>(a, c.blk, tid, r_src, r_dst);
+  }
+
   // ---- buffer descriptors (one expert's slice for the weights) ------------
   const int64_t expert_cols = (int64_t)c.e * a.N;
   const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w + expert_cols * khalf, (uint32_t)a.N * khalf);
@@ -274,16 +312,20 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   static_assert((BMX * UPR) % NT == 0, "staging units must divide evenly over the threads");
   uint32_t x_off[XU];
   int x_lds[XU];   // LDS byte offset within a buffer
+  // reads the tile's source rows from LDS (s_src), so only after they are there
+  auto init_x = [&]() {
 #pragma unroll
-  for (int j = 0; j < XU; ++j) {
-    const int u = tid + j * NT;
-    const int q = u / UPR;
-    const int cu = u - q * UPR;
-    const int row = row_of_group<UPR>(q);
-    const int src = s_src[row];
-    x_off[j] = src >= 0 ? (uint32_t)(src * a.ldx) + (uint32_t)(cu * 16) : kOOB;
-    x_lds[j] = row * PITCH + unit_pos<GS>(cu);
-  }
+    for (int j = 0; j < XU; ++j) {
+      const int u = tid + j * NT;
+      const int q = u / UPR;
+      const int cu = u - q * UPR;
+      const int row = row_of_group<UPR>(q);
+      const int src = s_src[row];
+      x_off[j] = src >= 0 ? (uint32_t)(src * a.ldx) + (uint32_t)(cu * 16) : kOOB;
+      x_lds[j] = row * PITCH + unit_pos<GS>(cu);
+    }
+  };
+  if constexpr (BM >= 64) init_x();
 
   // ---- the tile's zero points and scales -> registers (ZS_LDS) -------------
   // [BN columns x G] of each, contiguous from column tile_col0; the
@@ -313,20 +355,29 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   for (int nb = 0; nb < NB; ++nb) zs_lds[nb] = (c.col0 - c.tile_col0 + nb * 16 + jl) * a.G;
 
   // ---- chunk loaders -----------------------------------------------------
-  u32x4 xr[XU];
+  // Decode tiles (16/32 rows) request a chunk's activations together with
+  // its weights, RD - 1 chunks ahead, into a ring of RD register sets. Loads
+  // complete in issue order, so the wait for the activations about to be
+  // staged then only covers loads issued before them -- the chunk's own and
+  // earlier ones -- and the later chunks' weights stay in flight. (With one
+  // register set the activations of chunk c + 1 were requested after the
+  // weights of chunk c + RD - 1, and staging them waited for those too.)
+  constexpr bool XDEEP = BM < 64;
+  constexpr int XR = XDEEP ? RD : 1;
+  u32x4 xr[XR][XU];
   // the chunk's K offset moves the descriptor (scalar work) rather than going
   // into the unchecked scalar offset: units past K in a partial last chunk of
   // the tensor's last row then read as zero instead of past its end
-  auto load_x = [&](int ch) {
+  auto load_x = [&](int ch, int slot) {
     const uint32_t base = (uint32_t)(ch * KC);
     const __amdgpu_buffer_rsrc_t r = make_rsrc(a.x + base, a.x_bytes - base);
 #pragma unroll
-    for (int j = 0; j < XU; ++j) xr[j] = __builtin_amdgcn_raw_buffer_load_b128(r, x_off[j], 0, 0);
+    for (int j = 0; j < XU; ++j) xr[slot][j] = __builtin_amdgcn_raw_buffer_load_b128(r, x_off[j], 0, 0);
   };
-  auto store_x = [&](int buf) {
+  auto store_x = [&](int buf, int slot) {
 #pragma unroll
     for (int j = 0; j < XU; ++j) {
-      const u32x4 v = xr[j];
+      const u32x4 v = xr[slot][j];
       if constexpr (REPACKED) {
         // the repacked weights unpack in natural K order: no relabel
         *reinterpret_cast<u32x4*>(s_x + buf * BUF + x_lds[j]) = v;
@@ -347,7 +398,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     float s[KCG][NB];   // !ZSV: scales
   };
   // ZSV: one window of ZW chunks (KW groups) of zero points (raw runs) and scales
-  constexpr int ZW = zs_window(KCG, RD);
+  constexpr int ZW = zs_window(KCG, RD, BM);
   constexpr int KW = ZW * KCG;
   struct ZsWin {
     uint32_t zr[NB][(KW + 3) / 4];
@@ -414,6 +465,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // small. Only symmetric tiles with an LDS zero/scale block (SYMT: scales
   // / 16, so a small bias) take this path; every other tile and kernel
   // keeps the plain int32 chain and a convert.
+  bool tile_sym = false;   // decode tiles: every zero point of the tile is 8 (set in the prologue)
   float bias[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) bias[nb] = 0.f;
@@ -439,8 +491,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           if constexpr (ZS_LDS) {
-            zv[nb] = s_zero[zs_lds[nb] + gg];
             sv[nb] = s_scale[zs_lds[nb] + gg];
+            if constexpr (XDEEP) {
+              // decode tiles: a tile whose zero points are all 8 skips the read
+              zv[nb] = 8;
+              if (!tile_sym) zv[nb] = s_zero[zs_lds[nb] + gg];
+            } else {
+              zv[nb] = s_zero[zs_lds[nb] + gg];
+            }
           } else if constexpr (ZSV) {
             zv[nb] = zero_of<KW>(zw.zr[nb], dd * KCG + g);
             sv[nb] = zw.s[dd * KCG + g][nb];
@@ -566,22 +624,56 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // chunks per tile, where the extra chunk costs more than the join (measured
   // on the decode points), so they skip the loads past the end.
   constexpr bool CLAMP = BM >= 64;
+  static_assert(CLAMP != XDEEP, "decode tiles run the deep ring, prefill tiles the clamped loop");
   const int last_chunk = c.nchunks - 1;
   const int last_win = (c.nchunks + ZW - 1) / ZW - 1;
   WChunk ring[RD];
   // zs_cur serves the current window; zs_next is loaded one window ahead and
   // copied in at each window start (after the activation wait, which has
-  // covered its load: it was issued before those activations)
+  // covered its load: it was issued before those activations). Decode tiles
+  // instead keep one window (= one chunk, see zs_window) per ring slot.
   ZsWin zs_cur, zs_next;
-  if constexpr (!ZS_LDS && ZSV) load_zs(0, zs_next);
-  load_x(0);
+  ZsWin zs_ring[XDEEP && !ZS_LDS && ZSV ? RD : 1];
+  float r_xs = 0.f, r_tw = 1.f;   // decode tiles: this thread's row factors, to LDS in the epilogue
+  if constexpr (XDEEP) {
+    // chunks 0 .. RD - 2 in flight before the loop: the weights (and zero
+    // point / scale runs) first, right after the routing-row loads; then the
+    // rows go to LDS -- that wait covers only the row loads, issued first --
+    // and the row scales are requested (needed only by the epilogue); then,
+    // after the barrier that publishes the rows, the activations
 #pragma unroll
-  for (int d = 0; d < RD - 1; ++d) {
-    if constexpr (CLAMP) {
-      load_w(min(d, last_chunk), ring[d]);
-    } else {
-      if (d < c.nchunks) load_w(d, ring[d]);
+    for (int d = 0; d < RD - 1; ++d) {
+      if (d < c.nchunks) {
+        if constexpr (!ZS_LDS && ZSV) load_zs(d, zs_ring[d]);
+        load_w(d, ring[d]);
+      }
     }
+    if (tid < BM) {
+      s_src[tid] = r_src;
+      s_dst[tid] = r_dst;
+      if (r_dst >= 0) row_scales<ROUTED, DEBUGP>(a, r_src, r_dst, r_xs, r_tw);
+    }
+    // the tile's zero points (loaded for its LDS block, before the weights)
+    // all 8? Columns past N read zero: such a tile is not taken as symmetric.
+    int zok = ZS_LDS ? 1 : 0;
+    if constexpr (ZS_LDS) {
+#pragma unroll
+      for (int j = 0; j < ZU; ++j) {
+        const u32x4 q = zq[j];
+        if (tid + j * NT < z_units)
+          zok &= (q.x == 0x08080808u) & (q.y == 0x08080808u) & (q.z == 0x08080808u) & (q.w == 0x08080808u);
+      }
+    }
+    tile_sym = __syncthreads_and(zok) != 0;
+    init_x();
+#pragma unroll
+    for (int d = 0; d < RD - 1; ++d)
+      if (d < c.nchunks) load_x(d, d);
+  } else {
+    if constexpr (!ZS_LDS && ZSV) load_zs(0, zs_next);
+    load_x(0, 0);
+#pragma unroll
+    for (int d = 0; d < RD - 1; ++d) load_w(min(d, last_chunk), ring[d]);
   }
   if constexpr (ZS_LDS) {
     // visible to all waves after the first barrier of the loop; a symmetric
@@ -633,24 +725,24 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         __builtin_amdgcn_s_setprio(1);
         compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
         __builtin_amdgcn_s_setprio(0);
-        store_x((cc + 1) & 1);
-        load_x(min(cc + 2, last_chunk));
+        store_x((cc + 1) & 1, 0);
+        load_x(min(cc + 2, last_chunk), 0);
         load_w(min(cc + 2, last_chunk), ring[d]);
       } else {
-        load_x(min(cc + 1, last_chunk));
+        load_x(min(cc + 1, last_chunk), 0);
         load_w(min(cc + 1, last_chunk), ring[(d + 1) % 2]);
         __builtin_amdgcn_s_setprio(1);
         compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
         __builtin_amdgcn_s_setprio(0);
-        store_x((cc + 1) & 1);
+        store_x((cc + 1) & 1, 0);
       }
       __syncthreads();
     };
     // two separate loops (no join inside either, so no waits for loads there)
     if (((tid >> 6) >> 1) & 1) {
       // one more chunk in flight: A(1) in registers, W(1) in the ring
-      store_x(0);
-      load_x(min(1, last_chunk));
+      store_x(0, 0);
+      load_x(min(1, last_chunk), 0);
       load_w(min(1, last_chunk), ring[1]);
       __syncthreads();
       for (int ch = 0; ch < c.nchunks; ch += 2) {
@@ -659,7 +751,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         rebase();
       }
     } else {
-      store_x(0);
+      store_x(0, 0);
       __syncthreads();
       for (int ch = 0; ch < c.nchunks; ch += 2) {
         interval(ch, 0, std::false_type{});
@@ -668,26 +760,44 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       }
     }
   }
-  for (int ch = 0; ch < (STAGGER ? 0 : c.nchunks); ch += RD) {
+  if constexpr (XDEEP) {
+    // Decode loop: chunk cc (ring slot cc % RD = d) is staged from the
+    // registers its loads filled RD - 1 intervals earlier; after the barrier
+    // chunk cc + RD - 1 is requested into the slot chunk cc - 1 has freed.
+    for (int ch = 0; ch < c.nchunks; ch += RD) {
+#pragma unroll
+      for (int d = 0; d < RD; ++d) {
+        const int cc = ch + d;
+        if (FAST || cc < c.nchunks) {
+          store_x(cc & 1, d);
+          __syncthreads();
+          const int nx = cc + RD - 1, slot = (d + RD - 1) % RD;
+          if (nx < c.nchunks) {
+            if constexpr (!ZS_LDS && ZSV) load_zs(nx, zs_ring[slot]);
+            load_x(nx, slot);
+            load_w(nx, ring[slot]);
+          }
+          compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_ring[(!ZS_LDS && ZSV) ? d : 0], 0);
+        }
+      }
+      rebase();
+    }
+  }
+  for (int ch = 0; ch < (STAGGER || XDEEP ? 0 : c.nchunks); ch += RD) {
 #pragma unroll
     for (int d = 0; d < RD; ++d) {
       const int cc = ch + d;
       if (FAST || cc < c.nchunks) {
-        store_x(cc & 1);
+        store_x(cc & 1, 0);
         __syncthreads();
         if constexpr (!ZS_LDS && ZSV) {
           if (d % ZW == 0) {
             zs_cur = zs_next;
-            if (CLAMP || cc / ZW + 1 <= last_win) load_zs(min(cc / ZW + 1, last_win), zs_next);
+            load_zs(min(cc / ZW + 1, last_win), zs_next);
           }
         }
-        if constexpr (CLAMP) {
-          load_x(min(cc + 1, last_chunk));
-          load_w(min(cc + RD - 1, last_chunk), ring[(d + RD - 1) % RD]);
-        } else {
-          if (cc + 1 < c.nchunks) load_x(cc + 1);
-          if (cc + RD - 1 < c.nchunks) load_w(cc + RD - 1, ring[(d + RD - 1) % RD]);
-        }
+        load_x(min(cc + 1, last_chunk), 0);
+        load_w(min(cc + RD - 1, last_chunk), ring[(d + RD - 1) % RD]);
         // the 8-wave kernel's half- and quarter-height bodies raise their
         // priority for the compute phase as the staggered loop does (-0.8 %
         // on DeepSeek-V3 up M=4096 over five interleaved runs); in the 4-wave
@@ -702,6 +812,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 
   // (the reference-layout debug export passes no output)
   if (!DEBUGP || a.out != nullptr) {
+    if constexpr (XDEEP) {
+      // the row factors requested in the prologue (s_xs / s_tw are not used
+      // before the epilogue)
+      if (tid < BM) {
+        s_xs[tid] = r_xs;
+        s_tw[tid] = r_tw;
+      }
+      __syncthreads();
+    }
     // 128-column tiles: the finished tile goes through LDS (the activation
     // buffers are free now) so that every row leaves as 16-byte stores of
     // its 256 contiguous bytes -- 8 store instructions per wave instead of 64
@@ -773,6 +892,89 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   }
 }
 
+// Entry of a 64/128-row tile (block b, column tile nt, expert e): routing
+// rows and, with an LDS zero/scale block, the tile's symmetric check, then
+// the full-, half- or quarter-height body.
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST, bool ZSV>
+__device__ __forceinline__ void prefill_tile_impl(const GemmArgs& a, int b, int nt, int e, int wave, int8_t* s_x,
+                                                  float* s_scale, int8_t* s_zero, int* s_src, int* s_dst,
+                                                  float* s_xs, float* s_tw) {
+  constexpr int BN = NW * WN;
+  constexpr bool ROUTED = RMODE != 0;
+  const int tid = threadIdx.x;
+  __shared__ int s_rows;   // rows of the tile holding data
+  if (tid == 0) s_rows = 0;
+  __syncthreads();
+  // Tiles with an LDS zero/scale block: is every zero point of the tile's
+  // [BN x G] block 8 (symmetric int4)? The loads go out with the routing
+  // rows' and are checked at the same barrier. Columns past N read zero
+  // (not symmetric).
+  constexpr bool SYM_CHECK = ZSG > 0;
+  constexpr int ZCU = SYM_CHECK ? (BN * ZSG / 16 + NW * 64 - 1) / (NW * 64) : 1;
+  int zok = 1;
+  if constexpr (SYM_CHECK) {
+    const __amdgpu_buffer_rsrc_t zr = make_rsrc(a.wz + (int64_t)e * a.N * a.G, (uint32_t)(a.N * a.G));
+    const int z_units = BN * a.G / 16;
+#pragma unroll
+    for (int j = 0; j < ZCU; ++j) {
+      const int u = tid + j * NW * 64;
+      if (u < z_units) {
+        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(zr, (uint32_t)(nt * BN * a.G) + u * 16u, 0, 0);
+        zok &= (q.x == 0x08080808u) & (q.y == 0x08080808u) & (q.z == 0x08080808u) & (q.w == 0x08080808u);
+      }
+    }
+  }
+  if (tid < BM) {
+    int src, dst;
+    float xsv = 0.f, twv = 1.f;
+    row_source<BM, ROUTED>(a, b, tid, src, dst);
+    if (dst >= 0) row_scales<ROUTED, DEBUGP>(a, src, dst, xsv, twv);
+    s_src[tid] = src;
+    s_dst[tid] = dst;
+    s_xs[tid] = xsv;
+    s_tw[tid] = twv;
+    if (dst >= 0) atomicMax(&s_rows, tid + 1);
+  }
+  const bool tsym = SYM_CHECK ? __syncthreads_and(zok) != 0 : (__syncthreads(), false);
+  const int rows = __builtin_amdgcn_readfirstlane(s_rows);
+
+  TileCtx c;
+  c.e = e;
+  c.blk = b;
+  c.tile_col0 = nt * BN;
+  c.col0 = nt * BN + wave * WN;
+  c.nchunks = (a.G + KCG - 1) / KCG;
+  c.rows = rows;
+  // tiles whose valid rows fit in the top quarter (8-wave 128-row tiles: the
+  // second block of most DeepSeek-V3 experts) or half run a shorter body;
+  // symmetric tiles run the magic-number fold (SYMT)
+  auto run = [&](auto symt_c) {
+    constexpr bool SYMT = decltype(symt_c)::value;
+    if constexpr (BM >= 128 && NW == 8) {
+      if (rows <= BM / 4) {
+        gemm_body<BM / 4, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero,
+                                                                                    s_src, s_dst, s_xs, s_tw);
+        return;
+      }
+    }
+    if constexpr (BM >= 64) {
+      if (rows <= BM / 2) {
+        gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero,
+                                                                                    s_src, s_dst, s_xs, s_tw);
+        return;
+      }
+    }
+    gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero, s_src,
+                                                                            s_dst, s_xs, s_tw);
+  };
+  if constexpr (SYM_CHECK) {
+    if (tsym) run(std::true_type{});
+    else run(std::false_type{});
+  } else {
+    run(std::false_type{});
+  }
+}
+
 // ZSG > 0: zero points and scales come from an LDS copy of the tile's
 // block; the host launches this only when G <= ZSG (see zs_block_fits).
 template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST, bool ZSV,
@@ -792,7 +994,6 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   __shared__ int s_dst[BM];
   __shared__ float s_xs[BM];
   __shared__ float s_tw[BM];
-  __shared__ int s_rows;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -835,87 +1036,23 @@ void w4a8_gemm_kernel(const GemmArgs a) {
     if (e < 0) return;
   }
 
-  if (tid == 0) s_rows = 0;
-  __syncthreads();
-  // Tiles with an LDS zero/scale block: is every zero point of the tile's
-  // [BN x G] block 8 (symmetric int4)? The loads go out with the routing
-  // rows' and are checked at the same barrier. Columns past N read zero
-  // (not symmetric).
-  constexpr bool SYM_CHECK = ZSG > 0;
-  constexpr int ZCU = SYM_CHECK ? (BN * ZSG / 16 + NW * 64 - 1) / (NW * 64) : 1;
-  int zok = 1;
-  if constexpr (SYM_CHECK) {
-    const __amdgpu_buffer_rsrc_t zr = make_rsrc(a.wz + (int64_t)e * a.N * a.G, (uint32_t)(a.N * a.G));
-    const int z_units = BN * a.G / 16;
-#pragma unroll
-    for (int j = 0; j < ZCU; ++j) {
-      const int u = tid + j * NW * 64;
-      if (u < z_units) {
-        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(zr, (uint32_t)(nt * BN * a.G) + u * 16u, 0, 0);
-        zok &= (q.x == 0x08080808u) & (q.y == 0x08080808u) & (q.z == 0x08080808u) & (q.w == 0x08080808u);
-      }
-    }
-  }
-  if (tid < BM) {
-    int src = -1, dst = -1;
-    float xsv = 0.f, twv = 1.f;
-    if constexpr (ROUTED) {
-      const int s = a.sorted_ids[b * BM + tid];
-      if (s >= 0 && s < a.num_pairs) {
-        src = s / a.topk;
-        dst = s;
-        xsv = a.xs[src];
-        twv = a.tw ? a.tw[s] : 1.f;
-      }
-    } else {
-      const int r = a.blk_row0[b] + tid;
-      if (r < a.blk_row1[b]) {
-        src = dst = r;
-        if (!DEBUGP || a.xs != nullptr) xsv = a.xs[r];   // the debug export may pass no scales
-      }
-    }
-    s_src[tid] = src;
-    s_dst[tid] = dst;
-    s_xs[tid] = xsv;
-    s_tw[tid] = twv;
-    if (dst >= 0) atomicMax(&s_rows, tid + 1);
-  }
-  const bool tsym = SYM_CHECK ? __syncthreads_and(zok) != 0 : (__syncthreads(), false);
-  const int rows = __builtin_amdgcn_readfirstlane(s_rows);
-
-  TileCtx c;
-  c.e = e;
-  c.tile_col0 = nt * BN;
-  c.col0 = nt * BN + wave * WN;
-  c.nchunks = (a.G + KCG - 1) / KCG;
-  c.rows = rows;
-  // tiles whose valid rows fit in the top quarter (8-wave 128-row tiles: the
-  // second block of most DeepSeek-V3 experts) or half run a shorter body;
-  // symmetric tiles run the magic-number fold (SYMT)
-  auto run = [&](auto symt_c) {
-    constexpr bool SYMT = decltype(symt_c)::value;
-    if constexpr (BM >= 128 && NW == 8) {
-      if (rows <= BM / 4) {
-        gemm_body<BM / 4, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero,
-                                                                                    s_src, s_dst, s_xs, s_tw);
-        return;
-      }
-    }
-    if constexpr (BM >= 64) {
-      if (rows <= BM / 2) {
-        gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero,
-                                                                                    s_src, s_dst, s_xs, s_tw);
-        return;
-      }
-    }
-    gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero, s_src,
-                                                                            s_dst, s_xs, s_tw);
-  };
-  if constexpr (SYM_CHECK) {
-    if (tsym) run(std::true_type{});
-    else run(std::false_type{});
+  if constexpr (BM < 64) {
+    // Decode tiles request their first weight chunks before the routing
+    // rows are read (the body loads those itself); they decide the
+    // symmetric unpack per group and keep the plain int32 fold -- at these
+    // sizes the weight stream, not the fold, sets the time.
+    TileCtx c;
+    c.e = e;
+    c.blk = b;
+    c.tile_col0 = nt * BN;
+    c.col0 = nt * BN + wave * WN;
+    c.nchunks = (a.G + KCG - 1) / KCG;
+    c.rows = BM;
+    gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, false>(a, c, s_x, s_scale, s_zero, s_src,
+                                                                              s_dst, s_xs, s_tw);
   } else {
-    run(std::false_type{});
+    prefill_tile_impl<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV>(a, b, nt, e, wave, s_x, s_scale, s_zero,
+                                                                           s_src, s_dst, s_xs, s_tw);
   }
 }
 
@@ -943,7 +1080,7 @@ static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   // a column's zero points / scales of one window can be read as one aligned
   // run when G is a multiple of the window's groups and both tensors are
   // 16-byte aligned
-  a.zs_vec = (a.G % (KCG * zs_window(KCG, RD)) == 0) && (reinterpret_cast<uintptr_t>(a.wz) % 16 == 0) &&
+  a.zs_vec = (a.G % (KCG * zs_window(KCG, RD, BM)) == 0) && (reinterpret_cast<uintptr_t>(a.wz) % 16 == 0) &&
              (reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
   // output rows can be written in 16-byte pieces
   a.vec_out = (a.N % 8 == 0) && (a.ldo % 8 == 0) && (reinterpret_cast<uintptr_t>(a.out) % 16 == 0);

@@ -148,6 +148,9 @@ hipError_t launch_router_topk(const float* logits, int64_t ld, int M, int E, int
                               float* weights, hipStream_t s);
 hipError_t launch_combine_topk(const uint16_t* y, int64_t ldy, int M, int topk, int N, const float* weights,
                                uint16_t* out, int64_t ldo, hipStream_t s);
+// Streaming read of `bytes` (a multiple of 16) at src with `blocks`
+// 256-thread workgroups; sink receives at most 4096 bytes (measure.hip).
+hipError_t launch_stream_read(const void* src, int64_t bytes, void* sink, int blocks, hipStream_t s);
 // Weight repack between the reference int4 packing and the MFMA order
 // (inverse != 0: back to the reference packing); n_words 32-bit words.
 hipError_t launch_repack_weights(const uint32_t* src, uint32_t* dst, int64_t n_words, int inverse, hipStream_t s);

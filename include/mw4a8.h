@@ -251,6 +251,17 @@ int mw4a8_combine_topk(const uint16_t* y_bf16, int64_t ldy, int M, int topk, int
                        uint16_t* out_bf16, int64_t ldo, void* stream);
 
 /*
+ * Measurement utility (no reference counterpart): reads `bytes` of device
+ * memory at src (16-byte aligned, a multiple of 16) once, with coalesced
+ * 16-byte loads, eight in flight per thread, `blocks` workgroups of 256
+ * threads in a grid-stride loop. Its rate is the ceiling the benchmark sets
+ * memory-bound GEMM points against. sink: device buffer of at least 4096
+ * bytes (written only in the unlikely case that the XOR of the data equals a
+ * fixed constant). blocks in [1, 65536].
+ */
+int mw4a8_stream_read(const void* src, int64_t bytes, void* sink, size_t sink_bytes, int blocks, void* stream);
+
+/*
  * CPU-only self-test of the operand packing helpers the kernels use
  * (zero-point fold over all 16 x 256 nibble/zero pairs, the K relabelling
  * of activations vs weights, bf16 rounding). Returns 0 on success, else the

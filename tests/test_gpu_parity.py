@@ -173,9 +173,12 @@ def test_routed_partials_repacked_bit_exact(pkg, dev, bm):
         assert torch.equal(part[pe], task1_ref.group_partials(x_q[pe], w_e, gs).to(torch.int32)), f"expert {e}"
 
 
-@pytest.mark.parametrize("gs,bm", [(64, 16), (64, 64), (64, 128), (256, 16), (256, 64), (256, 128)])
+@pytest.mark.parametrize("gs,bm", [(64, 16), (64, 64), (64, 128), (256, 16), (256, 64), (256, 128), (128, 16),
+                                   (128, 64)])
 def test_routed_partials_other_group_sizes(pkg, dev, gs, bm):
-    """Group sizes 64 and 256 through the routed 16/64/128-row bodies."""
+    """Group sizes 64 and 256 through the routed 16/64/128-row bodies, and
+    tiles of every group size whose zero points mix 8 with others (the
+    decode tiles then take the per-group symmetric check)."""
     loads = [129, 70, 20]
     N, K = 256, 4608 if gs == 256 else 4096
     x_q, x_scale, w_q4, w_scale, w_zero, ids, tw = _routed_partials_case(pkg, loads, N, K, gs, "symmetric", gs + bm)
@@ -592,3 +595,20 @@ def test_routed_unsorted_expert_ids_never_mix_experts(pkg, dev):
     d = (out.float() - ref.float()).abs()[fin]
     bound = (1e-4 * N + 0.016 * ref.float().abs())[fin]
     assert bool((d <= bound).all()), "a written value differs from its expert's oracle value"
+
+
+def test_stream_read_utility(pkg, dev):
+    """The measurement kernel reads a buffer (sizes that end mid-grid) and
+    leaves its sink untouched for ordinary data."""
+    import ctypes
+    from flagos_kernel_gen_amd import _lib
+    L = _lib.lib()
+    sink = torch.zeros(4096, dtype=torch.uint8, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    for nbytes, blocks in ((16, 1), (4096 * 16 + 48, 3), (64 << 20, 2048), (64 << 20, 256)):
+        buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        rc = L.mw4a8_stream_read(ctypes.c_void_p(buf.data_ptr()), nbytes, ctypes.c_void_p(sink.data_ptr()), 4096,
+                                 blocks, stream)
+        assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    assert int(sink.sum()) == 0

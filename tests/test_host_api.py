@@ -209,3 +209,14 @@ def test_skewed_routing_meets_its_definition(pkg):
     load = torch.bincount(ids.reshape(-1).long(), minlength=256)
     assert float(load.max()) > 10 * 4096 * 8 / 256
     assert int((load == 0).sum()) >= 1
+
+
+def test_stream_read_utility_rejects_bad_arguments(pkg):
+    from flagos_kernel_gen_amd import _lib
+    L = _lib.lib()
+    p, q = ctypes.c_void_p(4096), ctypes.c_void_p(8192)
+    assert L.mw4a8_stream_read(p, 24, q, 4096, 256, None) == -1          # not a multiple of 16
+    assert L.mw4a8_stream_read(p, 1024, q, 1024, 256, None) == -1        # sink too small
+    assert L.mw4a8_stream_read(p, 1024, q, 4096, 0, None) == -1          # no workgroups
+    assert L.mw4a8_stream_read(ctypes.c_void_p(4100), 1024, q, 4096, 8, None) == -1   # misaligned
+    assert L.mw4a8_stream_read(p, 0, q, 4096, 8, None) == 0              # nothing to read
