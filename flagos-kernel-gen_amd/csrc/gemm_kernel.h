@@ -183,7 +183,11 @@ __device__ __forceinline__ int unit_pos(int cu) {
 // the window's scales fit in 8 registers, else one chunk.
 // Decode tiles (bm < 64) keep one chunk per window: each ring slot carries
 // its chunk's runs, requested with the chunk's weights.
-__host__ __device__ constexpr int zs_window(int kcg, int rd, int bm) { return bm < 64 ? 1 : (kcg * rd <= 8 ? rd : 1); }
+// Runs of 1, 2, 4 or 8 groups have a vector load (load_zero_run /
+// load_scale_run); other windows fall back to one chunk.
+__host__ __device__ constexpr int zs_window(int kcg, int rd, int bm) {
+  return bm < 64 ? 1 : ((kcg * rd <= 8 && (kcg * rd & (kcg * rd - 1)) == 0) ? rd : 1);
+}
 
 // Per-tile values shared by the kernel's setup and its tile bodies.
 struct TileCtx {
@@ -710,7 +714,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // its issue priority for its compute phase, so that a SIMD mate's loads and
   // staging fill the gaps rather than delay the MFMA chain (measured -0.75 %
   // over five interleaved runs).
-  constexpr bool STAGGER = NW == 8 && BMX == BM && RD == 2 && CLAMP;
+  constexpr bool STAGGER = NW == 8 && BMX == BM && CLAMP;
   if constexpr (STAGGER) {
     // one interval of chunk cc (ring parity d); LATE selects the order
     auto interval = [&](int cc, int d, auto late_tag) {
@@ -727,10 +731,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         __builtin_amdgcn_s_setprio(0);
         store_x((cc + 1) & 1, 0);
         load_x(min(cc + 2, last_chunk), 0);
-        load_w(min(cc + 2, last_chunk), ring[d]);
+        load_w(min(cc + RD, last_chunk), ring[d]);
       } else {
         load_x(min(cc + 1, last_chunk), 0);
-        load_w(min(cc + 1, last_chunk), ring[(d + 1) % 2]);
+        load_w(min(cc + RD - 1, last_chunk), ring[(d + RD - 1) % RD]);
         __builtin_amdgcn_s_setprio(1);
         compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
         __builtin_amdgcn_s_setprio(0);
@@ -738,76 +742,106 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       }
       __syncthreads();
     };
-    // two separate loops (no join inside either, so no waits for loads there)
-    if (((tid >> 6) >> 1) & 1) {
-      // one more chunk in flight: A(1) in registers, W(1) in the ring
-      store_x(0, 0);
-      load_x(min(1, last_chunk), 0);
-      load_w(min(1, last_chunk), ring[1]);
-      __syncthreads();
-      for (int ch = 0; ch < c.nchunks; ch += 2) {
-        interval(ch, 0, std::true_type{});
-        if (ch + 1 < c.nchunks) interval(ch + 1, 1, std::true_type{});
+    // Two separate loops (no join inside either, so no waits for loads
+    // there). Each loop iteration runs both intervals unconditionally and an
+    // odd last chunk runs after the loop: with the second interval under a
+    // condition, the loop header had a predecessor that issued no loads after
+    // the current weights, and the wait-count merge there made every other
+    // compute phase wait for the loads issued just before the barrier.
+    auto run_loop = [&](auto late_tag) {
+      int ch = 0;
+      for (; ch + RD <= c.nchunks; ch += RD) {
+#pragma unroll
+        for (int d = 0; d < RD; ++d) interval(ch + d, d, late_tag);
         rebase();
       }
+      if (ch < c.nchunks) {
+#pragma unroll
+        for (int d = 0; d < RD; ++d)
+          if (ch + d < c.nchunks) interval(ch + d, d, late_tag);
+        rebase();
+      }
+    };
+    if (((tid >> 6) >> 1) & 1) {
+      // one more chunk in flight: A(1) in registers, W(RD - 1) in the ring
+      store_x(0, 0);
+      load_x(min(1, last_chunk), 0);
+      load_w(min(RD - 1, last_chunk), ring[RD - 1]);
+      __syncthreads();
+      run_loop(std::true_type{});
     } else {
       store_x(0, 0);
       __syncthreads();
-      for (int ch = 0; ch < c.nchunks; ch += 2) {
-        interval(ch, 0, std::false_type{});
-        if (ch + 1 < c.nchunks) interval(ch + 1, 1, std::false_type{});
-        rebase();
-      }
+      run_loop(std::false_type{});
     }
   }
   if constexpr (XDEEP) {
     // Decode loop: chunk cc (ring slot cc % RD = d) is staged from the
     // registers its loads filled RD - 1 intervals earlier; after the barrier
     // chunk cc + RD - 1 is requested into the slot chunk cc - 1 has freed.
-    for (int ch = 0; ch < c.nchunks; ch += RD) {
+    // The main loop runs while every such request exists, so it holds no
+    // conditional load (a join after one makes the wait-count merge assume
+    // the fewest loads in flight); the last chunks follow in a guarded tail.
+    auto step = [&](int cc, int d, bool load_next) {
+      store_x(cc & 1, d);
+      __syncthreads();
+      const int nx = cc + RD - 1, slot = (d + RD - 1) % RD;
+      if (load_next) {
+        if constexpr (!ZS_LDS && ZSV) load_zs(nx, zs_ring[slot]);
+        load_x(nx, slot);
+        load_w(nx, ring[slot]);
+      }
+      compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_ring[(!ZS_LDS && ZSV) ? d : 0], 0);
+    };
+    int ch = 0;
+    for (; ch + 2 * RD - 1 <= c.nchunks; ch += RD) {
+#pragma unroll
+      for (int d = 0; d < RD; ++d) step(ch + d, d, true);
+      rebase();
+    }
+    for (; ch < c.nchunks; ch += RD) {
 #pragma unroll
       for (int d = 0; d < RD; ++d) {
         const int cc = ch + d;
-        if (FAST || cc < c.nchunks) {
-          store_x(cc & 1, d);
-          __syncthreads();
-          const int nx = cc + RD - 1, slot = (d + RD - 1) % RD;
-          if (nx < c.nchunks) {
-            if constexpr (!ZS_LDS && ZSV) load_zs(nx, zs_ring[slot]);
-            load_x(nx, slot);
-            load_w(nx, ring[slot]);
-          }
-          compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_ring[(!ZS_LDS && ZSV) ? d : 0], 0);
-        }
+        if (cc < c.nchunks) step(cc, d, cc + RD - 1 < c.nchunks);
       }
       rebase();
     }
   }
-  for (int ch = 0; ch < (STAGGER || XDEEP ? 0 : c.nchunks); ch += RD) {
-#pragma unroll
-    for (int d = 0; d < RD; ++d) {
-      const int cc = ch + d;
-      if (FAST || cc < c.nchunks) {
-        store_x(cc & 1, 0);
-        __syncthreads();
-        if constexpr (!ZS_LDS && ZSV) {
-          if (d % ZW == 0) {
-            zs_cur = zs_next;
-            load_zs(min(cc / ZW + 1, last_win), zs_next);
-          }
+  if constexpr (!STAGGER && !XDEEP) {
+    auto step = [&](int cc, int d) {
+      store_x(cc & 1, 0);
+      __syncthreads();
+      if constexpr (!ZS_LDS && ZSV) {
+        if (d % ZW == 0) {
+          zs_cur = zs_next;
+          load_zs(min(cc / ZW + 1, last_win), zs_next);
         }
-        load_x(min(cc + 1, last_chunk), 0);
-        load_w(min(cc + RD - 1, last_chunk), ring[(d + RD - 1) % RD]);
-        // the 8-wave kernel's half- and quarter-height bodies raise their
-        // priority for the compute phase as the staggered loop does (-0.8 %
-        // on DeepSeek-V3 up M=4096 over five interleaved runs); in the 4-wave
-        // 64-row kernel it measured 1-3 % slower
-        if constexpr (NW == 8) __builtin_amdgcn_s_setprio(1);
-        compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
-        if constexpr (NW == 8) __builtin_amdgcn_s_setprio(0);
       }
+      load_x(min(cc + 1, last_chunk), 0);
+      load_w(min(cc + RD - 1, last_chunk), ring[(d + RD - 1) % RD]);
+      // the 8-wave kernel's half- and quarter-height bodies raise their
+      // priority for the compute phase as the staggered loop does (-0.8 %
+      // on DeepSeek-V3 up M=4096 over five interleaved runs); in the 4-wave
+      // 64-row kernel it measured 1-3 % slower
+      if constexpr (NW == 8) __builtin_amdgcn_s_setprio(1);
+      compute(cc, s_x + (cc & 1) * BUF, ring[d], zs_cur, d % ZW);
+      if constexpr (NW == 8) __builtin_amdgcn_s_setprio(0);
+    };
+    // whole ring turns without conditions (see the staggered loop), then the
+    // remaining chunks
+    int ch = 0;
+    for (; ch + RD <= c.nchunks; ch += RD) {
+#pragma unroll
+      for (int d = 0; d < RD; ++d) step(ch + d, d);
+      rebase();
     }
-    rebase();
+    if (!FAST && ch < c.nchunks) {
+#pragma unroll
+      for (int d = 0; d < RD; ++d)
+        if (ch + d < c.nchunks) step(ch + d, d);
+      rebase();
+    }
   }
 
   // (the reference-layout debug export passes no output)
