@@ -52,13 +52,32 @@ EXTRA_FLAGS = {src: ["-mllvm", "-pragma-unroll-threshold=200000"]
                for src in ("gemm_debug_routed.hip", "gemm_debug_csr.hip", "gemm_debug_repacked.hip")}
 
 
+def resources_path(src: str) -> str:
+    """Per-kernel register / scratch / occupancy report of one source
+    (the compiler's kernel-resource-usage remarks, written by every build)."""
+    return os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".resources.txt")
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), "-x", "hip", *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), "-x", "hip", *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-Rpass-analysis=kernel-resource-usage",
+           "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
-    noise = [ln for ln in r.stderr.splitlines() if "packed-fp32-ops" not in ln and ln.strip()]
+    remarks, noise, in_remark = [], [], False
+    for ln in r.stderr.splitlines():
+        if "kernel-resource-usage" in ln:
+            remarks.append(ln)
+            in_remark = True
+        elif in_remark and (ln.lstrip().startswith("|") or ln.lstrip().split("|")[0].strip().isdigit()):
+            continue   # the source snippet printed under a remark
+        else:
+            in_remark = False
+            if "packed-fp32-ops" not in ln and ln.strip() and not ln.startswith("In file included from"):
+                noise.append(ln)
+    with open(resources_path(src), "w") as f:
+        f.write("\n".join(remarks) + "\n")
     if noise:
         sys.stderr.write(f"[build] {src}:\n" + "\n".join(noise) + "\n")
     return obj

@@ -1149,18 +1149,22 @@ static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
 template <int GS, int RMODE, bool DEBUGP>
 hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, hipStream_t s) {
   constexpr int K512 = 512 / GS > 0 ? 512 / GS : 1;     // groups per 512 bytes of K
-  constexpr int K1024 = 1024 / GS > 0 ? 1024 / GS : 1;
   constexpr int K256 = 256 / GS > 0 ? 256 / GS : 1;
   switch (c.BM) {
+    // Decode tiles: 512-byte K chunks (4 groups at group size 128), two in
+    // flight per wave, at least two waves per SIMD: measured best or within 2 %
+    // on every decode point (M = 1 to 64 of the DeepSeek-V3, Mixtral and Qwen3
+    // shapes). The two-wave floor also caps every variant at 256 registers
+    // (with a one-wave hint the group-size-64 bodies took 380 and ran one
+    // wave per SIMD).
     case 16:
-      // 4-group chunks (at group size 128), two in flight per wave, two waves
-      // per SIMD: measured best or within 2 % on every decode point (M = 1
-      // to 64 of the DeepSeek-V3, Mixtral and Qwen3 shapes)
       if (zs_block_fits(a, 64, 64)) return launch_one<16, 16, 4, GS, K512, 2, 64, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);
-      return launch_one<16, 16, 4, GS, K1024, 2, 0, RMODE, DEBUGP, 1>(a, max_blocks, c.R, s);
+      return launch_one<16, 16, 4, GS, K512, 2, 0, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);
     case 32:
-      if (zs_block_fits(a, 64, 64)) return launch_one<32, 16, 4, GS, K512, 2, 64, RMODE, DEBUGP, 1>(a, max_blocks, c.R, s);
-      return launch_one<32, 16, 4, GS, K512, 2, 0, RMODE, DEBUGP, 1>(a, max_blocks, c.R, s);
+      // (256-byte chunks without the LDS zero/scale block: the 512-byte one
+      // spilled at group size 64)
+      if (zs_block_fits(a, 64, 64)) return launch_one<32, 16, 4, GS, K512, 2, 64, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);
+      return launch_one<32, 16, 4, GS, K256, 2, 0, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);
     // three waves per SIMD fit the gs = 128 body without spills; the others keep two
     case 64:
       // G <= 16 (K <= 2048 at group size 128): the tile's [128 x G] zero/scale
@@ -1169,8 +1173,9 @@ hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, hipStrea
         return launch_one<64, 32, 4, GS, K256, 2, 16, RMODE, DEBUGP, GS == 128 ? 3 : 2>(a, max_blocks, c.R, s);
       return launch_one<64, 32, 4, GS, K256, 2, 0, RMODE, DEBUGP, GS == 128 ? 3 : 2>(a, max_blocks, c.R, s);
     case 128:
-      // group size 128: 8 waves x 32 columns, staggered (see STAGGER)
-      if constexpr (GS == 128) {
+      // group sizes 128 and 256: 8 waves x 32 columns, staggered (see
+      // STAGGER; the 4-wave 256-row... body spilled at group size 256)
+      if constexpr (GS >= 128) {
         // the tile's whole [256 x G] zero-point/scale block in LDS when G <= 64
         // (80 KB beside the 72 KB of activation buffers: one tile per CU)
         if (zs_block_fits(a, 256, 64))

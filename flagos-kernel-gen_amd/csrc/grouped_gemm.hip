@@ -56,7 +56,7 @@ TileConfig tiles_for_block_m(int BM, int group_size) {
     case 16: c.WN = 16; c.KCG = 512 / group_size; c.R = 1; break;
     case 32: c.WN = 16; c.KCG = 512 / group_size; c.R = 1; break;
     case 64: c.WN = 32; c.KCG = 256 / group_size; c.R = 2; break;
-    default: c.BM = 128; c.WN = 32; c.KCG = 256 / group_size; c.R = 2; c.NW = group_size == 128 ? 8 : 4; break;
+    default: c.BM = 128; c.WN = 32; c.KCG = 256 / group_size; c.R = 2; c.NW = group_size >= 128 ? 8 : 4; break;
   }
   if (c.KCG < 1) c.KCG = 1;
   return c;
