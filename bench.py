@@ -414,7 +414,7 @@ def cpu_baseline(pkg, budget_s):
 
 def traffic_from_profiles():
     """HBM bytes per GEMM launch from the committed rocprofv3 PMC summary, if any."""
-    path = os.path.join(ROOT, "profiles", "traffic_dsv3_up_m4096.json")
+    path = os.path.join(ROOT, "profiles", "traffic_dsv3_up_4096.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
