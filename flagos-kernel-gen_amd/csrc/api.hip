@@ -100,8 +100,14 @@ GemmArgs base_args(const int8_t* x_q, int64_t ldx, int rows, const float* x_scal
   return a;
 }
 
-// Shared by the reference-layout GEMM and the debug export: build the block
-// table on the device, then launch.
+// Whether a reference-layout launch over E experts builds a block table in
+// the workspace: with up to kCsrScanExperts experts the GEMM's waves derive
+// their row blocks from the offsets themselves (one launch, no table).
+bool csr_uses_table(int E) { return E > kCsrScanExperts; }
+
+// Shared by the reference-layout GEMM and the debug export: the GEMM launch,
+// preceded by the block-table launch for many experts. The workspace is
+// required either way (its size depends on M_total and E only).
 int run_csr(GemmArgs a, const int32_t* offsets, int M_total, int E, int gs, void* workspace, size_t ws_bytes,
             hipStream_t s, bool debug) {
   if (!offsets) return fail(MW4A8_ERR_INVALID, "null expert_offsets");
@@ -114,14 +120,21 @@ int run_csr(GemmArgs a, const int32_t* offsets, int M_total, int E, int gs, void
     return fail(MW4A8_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", csr_ws_bytes(max_blocks),
                 workspace ? ws_bytes : (size_t)0);
   if (!aligned(workspace, 256)) return fail(MW4A8_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  CsrWorkspace w = carve(workspace, max_blocks);
-  hipError_t e = launch_csr_block_table(offsets, E, M_total, cfg.BM, max_blocks, w.expert, w.row0, w.row1,
-                                        w.count, s);
-  if (e != hipSuccess) return hip_fail(e, "block table launch");
-  a.blk_expert = w.expert;
-  a.blk_row0 = w.row0;
-  a.blk_row1 = w.row1;
-  a.blk_count = w.count;
+  hipError_t e;
+  a.E = E;
+  if (csr_uses_table(E)) {
+    CsrWorkspace w = carve(workspace, max_blocks);
+    e = launch_csr_block_table(offsets, E, M_total, cfg.BM, max_blocks, w.expert, w.row0, w.row1, w.count, s);
+    if (e != hipSuccess) return hip_fail(e, "block table launch");
+    a.blk_expert = w.expert;
+    a.blk_row0 = w.row0;
+    a.blk_row1 = w.row1;
+    a.blk_count = w.count;
+  } else {
+    a.offsets = offsets;
+    a.M_total = M_total;
+    a.max_blocks = max_blocks;
+  }
   e = debug ? launch_debug_partials(a, cfg, gs, kModeCsr, max_blocks, s)
             : launch_grouped_gemm(a, cfg, gs, kModeCsr, max_blocks, s);
   if (e != hipSuccess) return hip_fail(e, "grouped GEMM launch");
@@ -137,7 +150,8 @@ int run_csr(GemmArgs a, const int32_t* offsets, int M_total, int E, int gs, void
 // first call on a device resolves the device's own address of the array with
 // hipGetSymbolAddress, with that device current, and keeps it per device.
 // The block-table kernel writes every entry the GEMM reads, so nothing has
-// to be cleared between calls.
+// to be cleared between calls. Calls over at most kCsrScanExperts experts
+// build no table and leave the array untouched.
 constexpr int kNoallocMaxBlocks = 65536;
 constexpr size_t kNoallocScratchBytes = 256 + 3 * sizeof(int32_t) * (size_t)kNoallocMaxBlocks;   // 786688
 static_assert(kNoallocScratchBytes % 256 == 0, "scratch is whole 256-byte units");

@@ -193,27 +193,28 @@ __host__ __device__ constexpr int zs_window(int kcg, int rd, int bm) {
 struct TileCtx {
   int e;          // expert
   int blk;        // row block
+  int row0, row1; // reference layout: the block's rows [row0, row1)
   int col0;       // first column of this wave
   int tile_col0;  // first column of the workgroup's tile
   int nchunks;    // K-chunks
   int rows;       // rows of the tile holding data (the rest is padding)
 };
 
-// Row r of row block b: the activation row it reads (src) and the output
-// row it writes (dst), -1 for padding. Routed: the pair in slot b * BM + r
-// of sorted_ids; reference layout: row blk_row0[b] + r below blk_row1[b].
+// Row r of the tile's row block: the activation row it reads (src) and the
+// output row it writes (dst), -1 for padding. Routed: the pair in slot
+// blk * BM + r of sorted_ids; reference layout: row row0 + r below row1.
 template <int BM, bool ROUTED>
-__device__ __forceinline__ void row_source(const GemmArgs& a, int b, int r, int& src, int& dst) {
+__device__ __forceinline__ void row_source(const GemmArgs& a, const TileCtx& c, int r, int& src, int& dst) {
   src = dst = -1;
   if constexpr (ROUTED) {
-    const int s = a.sorted_ids[b * BM + r];
+    const int s = a.sorted_ids[c.blk * BM + r];
     if (s >= 0 && s < a.num_pairs) {
       src = s / a.topk;
       dst = s;
     }
   } else {
-    const int row = a.blk_row0[b] + r;
-    if (row < a.blk_row1[b]) src = dst = row;
+    const int row = c.row0 + r;
+    if (row < c.row1) src = dst = row;
   }
 }
 
@@ -288,7 +289,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // so waiting for these rows never waits for the weights requested next.
   int r_src = -1, r_dst = -1;
   if constexpr (BM < 64) {
-    if (tid < BM) row_source<BM, ROUTED>(a, c.blk, tid, r_src, r_dst);
+    if (tid < BM) row_source<BM, ROUTED>(a, c, tid, r_src, r_dst);
   }
 
   // ---- buffer descriptors (one expert's slice for the weights) ------------
@@ -926,13 +927,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   }
 }
 
-// Entry of a 64/128-row tile (block b, column tile nt, expert e): routing
-// rows and, with an LDS zero/scale block, the tile's symmetric check, then
-// the full-, half- or quarter-height body.
+// Entry of a 64/128-row tile (c: its block, rows, expert and columns):
+// routing rows and, with an LDS zero/scale block, the tile's symmetric
+// check, then the full-, half- or quarter-height body.
 template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST, bool ZSV>
-__device__ __forceinline__ void prefill_tile_impl(const GemmArgs& a, int b, int nt, int e, int wave, int8_t* s_x,
-                                                  float* s_scale, int8_t* s_zero, int* s_src, int* s_dst,
-                                                  float* s_xs, float* s_tw) {
+__device__ __forceinline__ void prefill_tile_impl(const GemmArgs& a, TileCtx c, int8_t* s_x, float* s_scale,
+                                                  int8_t* s_zero, int* s_src, int* s_dst, float* s_xs,
+                                                  float* s_tw) {
   constexpr int BN = NW * WN;
   constexpr bool ROUTED = RMODE != 0;
   const int tid = threadIdx.x;
@@ -947,13 +948,13 @@ __device__ __forceinline__ void prefill_tile_impl(const GemmArgs& a, int b, int 
   constexpr int ZCU = SYM_CHECK ? (BN * ZSG / 16 + NW * 64 - 1) / (NW * 64) : 1;
   int zok = 1;
   if constexpr (SYM_CHECK) {
-    const __amdgpu_buffer_rsrc_t zr = make_rsrc(a.wz + (int64_t)e * a.N * a.G, (uint32_t)(a.N * a.G));
+    const __amdgpu_buffer_rsrc_t zr = make_rsrc(a.wz + (int64_t)c.e * a.N * a.G, (uint32_t)(a.N * a.G));
     const int z_units = BN * a.G / 16;
 #pragma unroll
     for (int j = 0; j < ZCU; ++j) {
       const int u = tid + j * NW * 64;
       if (u < z_units) {
-        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(zr, (uint32_t)(nt * BN * a.G) + u * 16u, 0, 0);
+        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(zr, (uint32_t)(c.tile_col0 * a.G) + u * 16u, 0, 0);
         zok &= (q.x == 0x08080808u) & (q.y == 0x08080808u) & (q.z == 0x08080808u) & (q.w == 0x08080808u);
       }
     }
@@ -961,7 +962,7 @@ __device__ __forceinline__ void prefill_tile_impl(const GemmArgs& a, int b, int 
   if (tid < BM) {
     int src, dst;
     float xsv = 0.f, twv = 1.f;
-    row_source<BM, ROUTED>(a, b, tid, src, dst);
+    row_source<BM, ROUTED>(a, c, tid, src, dst);
     if (dst >= 0) row_scales<ROUTED, DEBUGP>(a, src, dst, xsv, twv);
     s_src[tid] = src;
     s_dst[tid] = dst;
@@ -971,13 +972,6 @@ __device__ __forceinline__ void prefill_tile_impl(const GemmArgs& a, int b, int 
   }
   const bool tsym = SYM_CHECK ? __syncthreads_and(zok) != 0 : (__syncthreads(), false);
   const int rows = __builtin_amdgcn_readfirstlane(s_rows);
-
-  TileCtx c;
-  c.e = e;
-  c.blk = b;
-  c.tile_col0 = nt * BN;
-  c.col0 = nt * BN + wave * WN;
-  c.nchunks = (a.G + KCG - 1) / KCG;
   c.rows = rows;
   // tiles whose valid rows fit in the top quarter (8-wave 128-row tiles: the
   // second block of most DeepSeek-V3 experts) or half run a shorter body;
@@ -1009,6 +1003,66 @@ __device__ __forceinline__ void prefill_tile_impl(const GemmArgs& a, int b, int 
   }
 }
 
+// Reference layout without a block table: the row blocks of expert e are
+// ceil((r1 - r0) / BM) blocks of rows [r0, r1) = its offsets clamped to
+// [0, M_total], laid out expert after expert -- the table
+// csr_block_table_kernel writes, derived by each wave on its own. Lane l of
+// chunk k holds expert 64 k + l: its clamped rows and the inclusive prefix
+// of the block counts. Returns the block count (wave-uniform).
+template <int BM>
+__device__ __forceinline__ int csr_scan(const GemmArgs& a, int (&r0)[kCsrScanChunks], int (&r1)[kCsrScanChunks],
+                                        int (&incl)[kCsrScanChunks]) {
+  const int lane = threadIdx.x & 63;
+  int lo[kCsrScanChunks], hi[kCsrScanChunks];
+#pragma unroll
+  for (int k = 0; k < kCsrScanChunks; ++k) {   // every load before the first use
+    const int e = k * 64 + lane;
+    lo[k] = hi[k] = 0;
+    if (e < a.E) {
+      lo[k] = a.offsets[e];
+      hi[k] = a.offsets[e + 1];
+    }
+  }
+  int carry = 0;
+#pragma unroll
+  for (int k = 0; k < kCsrScanChunks; ++k) {
+    r0[k] = min(max(lo[k], 0), a.M_total);
+    r1[k] = min(max(hi[k], 0), a.M_total);
+    int v = r1[k] > r0[k] ? (r1[k] - r0[k] + BM - 1) / BM : 0;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(v, d, 64);
+      if (lane >= d) v += o;
+    }
+    incl[k] = carry + v;
+    carry = __builtin_amdgcn_readlane(incl[k], 63);
+  }
+  return carry;
+}
+
+// Block b (< the count csr_scan returned) of that layout: its expert and
+// rows [row0, row1). The expert is the first lane whose inclusive prefix
+// exceeds b.
+template <int BM>
+__device__ __forceinline__ void csr_block(int b, const int (&r0)[kCsrScanChunks], const int (&r1)[kCsrScanChunks],
+                                          const int (&incl)[kCsrScanChunks], int& e, int& row0, int& row1) {
+  e = -1;
+  row0 = row1 = 0;
+#pragma unroll
+  for (int k = 0; k < kCsrScanChunks; ++k) {
+    const uint64_t m = __ballot(incl[k] > b);
+    if (e < 0 && m != 0) {
+      const int l = __builtin_ctzll(m);
+      const int lo = __builtin_amdgcn_readlane(r0[k], l);
+      const int hi = __builtin_amdgcn_readlane(r1[k], l);
+      const int first = __builtin_amdgcn_readlane(incl[k], l) - (hi - lo + BM - 1) / BM;
+      e = k * 64 + l;
+      row0 = lo + (b - first) * BM;
+      row1 = min(row0 + BM, hi);
+    }
+  }
+}
+
 // ZSG > 0: zero points and scales come from an LDS copy of the tile's
 // block; the host launches this only when G <= ZSG (see zs_block_fits).
 template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST, bool ZSV,
@@ -1037,9 +1091,12 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   // known here. Spread the actual tiles evenly over the 8 XCDs (workgroup L
   // runs on XCD L % 8), each XCD taking a contiguous run of the tile list.
   int nblocks;
+  int cs_r0[kCsrScanChunks], cs_r1[kCsrScanChunks], cs_incl[kCsrScanChunks];
   if constexpr (ROUTED) {
     // blocks past sorted_len / BM would read past sorted_ids / expert_ids
     nblocks = min(a.num_post_pad[0] / BM, a.sorted_len / BM);
+  } else if (a.offsets != nullptr) {
+    nblocks = min(csr_scan<BM>(a, cs_r0, cs_r1, cs_incl), a.max_blocks);
   } else {
     nblocks = a.blk_count[0];
   }
@@ -1052,7 +1109,7 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   if ((L >> 3) >= per_xcd) return;
   const int t = (L & 7) * per_xcd + (L >> 3);
   if (t >= tiles) return;
-  int b, nt, e;
+  int b, nt, e, row0 = 0, row1 = 0;
   if (egroups) {
     if (!expert_group_tile(t, a.n_tiles, a.R, nblocks, a.expert_ids, a.E, b, nt, e)) return;
   } else {
@@ -1064,29 +1121,35 @@ void w4a8_gemm_kernel(const GemmArgs a) {
     if constexpr (ROUTED) {
       e = a.expert_ids[b];
       if (e >= a.E) return;
+    } else if (a.offsets != nullptr) {
+      csr_block<BM>(b, cs_r0, cs_r1, cs_incl, e, row0, row1);
     } else {
       e = a.blk_expert[b];
+      row0 = a.blk_row0[b];
+      row1 = a.blk_row1[b];
     }
     if (e < 0) return;
   }
 
+  TileCtx c;
+  c.e = e;
+  c.blk = b;
+  c.row0 = row0;
+  c.row1 = row1;
+  c.tile_col0 = nt * BN;
+  c.col0 = nt * BN + wave * WN;
+  c.nchunks = (a.G + KCG - 1) / KCG;
+  c.rows = BM;
   if constexpr (BM < 64) {
     // Decode tiles request their first weight chunks before the routing
     // rows are read (the body loads those itself); they decide the
     // symmetric unpack per group and keep the plain int32 fold -- at these
     // sizes the weight stream, not the fold, sets the time.
-    TileCtx c;
-    c.e = e;
-    c.blk = b;
-    c.tile_col0 = nt * BN;
-    c.col0 = nt * BN + wave * WN;
-    c.nchunks = (a.G + KCG - 1) / KCG;
-    c.rows = BM;
     gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, false>(a, c, s_x, s_scale, s_zero, s_src,
                                                                               s_dst, s_xs, s_tw);
   } else {
-    prefill_tile_impl<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV>(a, b, nt, e, wave, s_x, s_scale, s_zero,
-                                                                           s_src, s_dst, s_xs, s_tw);
+    prefill_tile_impl<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV>(a, c, s_x, s_scale, s_zero, s_src,
+                                                                           s_dst, s_xs, s_tw);
   }
 }
 

@@ -21,6 +21,11 @@ struct GemmArgs {
   const int32_t* blk_row0;
   const int32_t* blk_row1;
   const int32_t* blk_count;   // [0] = number of valid blocks
+  // reference layout without a block table (E <= kCsrScanExperts): every
+  // wave derives its block from the clamped CSR offsets [E + 1] itself
+  const int32_t* offsets;
+  int M_total;
+  int max_blocks;             // blocks past this bound are dropped, as by the table
   // routed layout: block b covers sorted slots [b*BM, b*BM+BM)
   const int32_t* sorted_ids;
   const int32_t* expert_ids;
@@ -115,6 +120,11 @@ TileConfig tiles_for_block_m(int BM, int group_size);
 // Upper bound on the number of row blocks for `rows` rows spread over at
 // most `experts` experts: every expert adds at most one partial block.
 int max_row_blocks(int rows, int experts, int BM);
+
+// Experts up to which a reference-layout launch needs no block table: each
+// wave scans the offsets in chunks of 64 experts, one expert per lane.
+constexpr int kCsrScanChunks = 4;
+constexpr int kCsrScanExperts = 64 * kCsrScanChunks;
 
 // Kernel launchers; return hipSuccess or the launch error.
 hipError_t launch_csr_block_table(const int32_t* offsets, int E, int M_total, int BM, int max_blocks,

@@ -102,7 +102,11 @@ def test_align_out_of_range_ids_and_empty(pkg, dev):
     # 128-row 8-wave tiles at K >= 4096 (full, half and quarter bodies)
     (3, 700, 256, 4608, 128, "symmetric"), (3, 700, 256, 4608, 128, "full"),
     # group sizes 64 / 256 on 64- and 128-row tiles
-    (3, 300, 256, 1024, 64, "symmetric"), (2, 500, 128, 4096, 256, "symmetric")])
+    (3, 300, 256, 1024, 64, "symmetric"), (2, 500, 128, 4096, 256, "symmetric"),
+    # row blocks looked up by the waves' own scan of the offsets over all of
+    # its four 64-expert chunks (E = 256), and from the block table (E > 256)
+    (256, 3000, 64, 512, 128, "symmetric"), (256, 9000, 64, 512, 128, "full"),
+    (300, 3000, 64, 512, 128, "symmetric"), (300, 9000, 64, 512, 128, "full")])
 def test_debug_partials_bit_exact(pkg, dev, E, M, N, K, gs, zero):
     """The reference-layout export runs the tile mw4a8_grouped_gemm selects
     for the same problem; its int32 partials equal the oracle's exactly."""
@@ -238,6 +242,16 @@ def test_grouped_edge_cases(pkg, dev):
                                                                        zero="full")
     out, ref = _run_grouped(pkg, dev, x_q, x_scale, w_q4, w_scale, w_zero, offs, 64)
     assert_close(out, ref, 1400, "edge/N=1400 full zeros")
+    # many experts, most empty, some with several row blocks: the waves'
+    # offset scan (E <= 256) and the block table (E > 256) on the same rows
+    for E in (256, 257):
+        x_q, x_scale, w_q4, w_scale, w_zero, _ = wl.make_grouped_inputs(E, 600, 128, 512, 128, seed=80)
+        counts = torch.zeros(E, dtype=torch.int64)
+        counts[[0, 63, 64, 130, 191, 192, 255]] = torch.tensor([1, 70, 17, 200, 33, 150, 129])
+        offs = torch.zeros(E + 1, dtype=torch.int32)
+        offs[1:] = torch.cumsum(counts, 0).to(torch.int32)
+        out, ref = _run_grouped(pkg, dev, x_q, x_scale, w_q4, w_scale, w_zero, offs, 128)
+        assert_close(out, ref, 128, f"edge/sparse E={E}")
     # activation rows with a stride larger than K
     x_q, x_scale, w_q4, w_scale, w_zero, offs = wl.make_grouped_inputs(4, 33, 512, 1024, 128, seed=80)
     big = torch.zeros(33, 1024 + 64, dtype=torch.int8, device=dev)

@@ -2,7 +2,9 @@
 through the C ABI: its output equals that of ``mw4a8_grouped_gemm`` (the same
 kernels, with a caller workspace) bit for bit, on two calls in a row, the
 second with a smaller input (fewer row blocks than the first left in the
-shared scratch array), and both match the oracle."""
+shared scratch array, which holds the row-block table of calls over more
+than 256 experts), and both match the oracle; then on two calls over fewer
+experts, whose kernels find their row blocks without the table."""
 
 import ctypes
 
@@ -23,8 +25,12 @@ def test_noalloc_matches_workspace_entry(pkg, dev, order):
     from flagos_kernel_gen_amd import _lib
     L = _lib.lib()
     stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-    # 128-row tiles (150 rows per expert at K = 4608), then 16-row tiles
-    cases = [(8, 1200, 512, 4608, 128, 11), (4, 40, 384, 1024, 128, 12)]
+    # Over more than 256 experts the row-block table lives in the scratch
+    # array: a larger table, then a smaller one over the first's leftovers.
+    # Then calls that derive the blocks in the kernel (128-row tiles at
+    # 150 rows per expert and K = 4608, then 16-row tiles).
+    cases = [(300, 6000, 256, 1024, 128, 13), (260, 700, 256, 512, 128, 14),
+             (8, 1200, 512, 4608, 128, 11), (4, 40, 384, 1024, 128, 12)]
     for E, M, N, K, gs, seed in cases:
         print(f"[noalloc] E={E} M={M} N={N} K={K}", flush=True)
         x_q, x_scale, w_q4, w_scale, w_zero, offs = pkg.workloads.make_grouped_inputs(E, M, N, K, gs, seed=seed)
