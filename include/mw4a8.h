@@ -46,7 +46,8 @@ int mw4a8_abi_version(void);
 
 /*
  * Bytes of device workspace mw4a8_grouped_gemm / mw4a8_debug_partials need
- * for this problem (a per-call block table; 256-byte aligned size).
+ * for this problem (a per-call block table, written only when E > 256; the
+ * workspace is required for every E; 256-byte aligned size).
  */
 size_t mw4a8_workspace_bytes(int M_total, int N, int K, int E, int group_size);
 
@@ -78,13 +79,15 @@ int mw4a8_grouped_gemm(const int8_t* x_q, int64_t ldx, const float* x_scale, con
  * workspace argument. No counterpart in the reference; for callers that
  * cannot allocate device memory (code under HIP-graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). Same arguments, kernels and
- * results as mw4a8_grouped_gemm; its per-call block table lives in a fixed
- * device array of the library (786688 bytes per GPU, held until the process
- * ends) that bounds a call to 65536 row blocks -- about 65536 rows (fewer
- * when experts end in partial blocks); larger calls return
- * MW4A8_ERR_UNSUPPORTED. The stream must belong to the current device. Every
- * call on one GPU shares that array: calls that overlap on one GPU (e.g. on
- * two streams at once) race and must be ordered by the caller.
+ * results as mw4a8_grouped_gemm. Over more than 256 experts its per-call
+ * block table lives in a fixed device array of the library (786688 bytes per
+ * GPU, held until the process ends); over fewer the kernels find their row
+ * blocks from expert_offsets and the array is not used. A call is bounded to
+ * 65536 row blocks -- about 65536 rows (fewer when experts end in partial
+ * blocks); larger calls return MW4A8_ERR_UNSUPPORTED. The stream must belong
+ * to the current device. Every call on one GPU shares that array: calls over
+ * more than 256 experts that overlap on one GPU (e.g. on two streams at
+ * once) race and must be ordered by the caller.
  */
 int mw4a8_grouped_gemm_noalloc(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
                                const float* w_scale, const int8_t* w_zero, const int32_t* expert_offsets,

@@ -524,8 +524,8 @@ def test_routed_config_points(pkg, dev, name, M):
 
 def test_graph_capture_replays(pkg, dev):
     """Both entries captured in one HIP graph (the routed call with its
-    internal routing kernel, the reference-layout call with its block-table
-    kernel) and replayed three times with new input values copied into the
+    internal routing kernel, the reference-layout call) and replayed three
+    times with new input values copied into the
     captured tensors. Between replays, eager calls of other sizes on the same
     stream make the wrapper's cached routing buffer and workspace grow, which
     frees the buffers they replace; every replay must still match the oracle.
