@@ -198,7 +198,28 @@ struct TileCtx {
   int tile_col0;  // first column of the workgroup's tile
   int nchunks;    // K-chunks
   int rows;       // rows of the tile holding data (the rest is padding)
+  int tail;       // routed tiles with a tail: the block whose first slots follow this block's rows, or -1
 };
+
+// Routed slot s of sorted_ids: the pair's activation row (src) and output row
+// (dst), or -1 for padding.
+__device__ __forceinline__ void routed_slot(const GemmArgs& a, int slot, int& src, int& dst) {
+  src = dst = -1;
+  const int s = a.sorted_ids[slot];
+  if (s >= 0 && s < a.num_pairs) {
+    src = s / a.topk;
+    dst = s;
+  }
+}
+
+// Routed block x holds at most T pairs: its slot T is padding. (An expert's
+// pairs fill its blocks from the first slot on, so only its last block can
+// be short, and its pairs are that block's first slots.)
+template <int BM, int T>
+__device__ __forceinline__ bool short_block(const GemmArgs& a, int x) {
+  const int s = a.sorted_ids[x * BM + T];
+  return s < 0 || s >= a.num_pairs;
+}
 
 // Row r of the tile's row block: the activation row it reads (src) and the
 // output row it writes (dst), -1 for padding. Routed: the pair in slot
@@ -207,11 +228,7 @@ template <int BM, bool ROUTED>
 __device__ __forceinline__ void row_source(const GemmArgs& a, const TileCtx& c, int r, int& src, int& dst) {
   src = dst = -1;
   if constexpr (ROUTED) {
-    const int s = a.sorted_ids[c.blk * BM + r];
-    if (s >= 0 && s < a.num_pairs) {
-      src = s / a.topk;
-      dst = s;
-    }
+    routed_slot(a, c.blk * BM + r, src, dst);
   } else {
     const int row = c.row0 + r;
     if (row < c.row1) src = dst = row;
@@ -254,7 +271,7 @@ __device__ __forceinline__ void row_scales(const GemmArgs& a, int src, int dst, 
 //     join, and waited there for every outstanding load, which serialized
 //     the prefetch with the compute.
 template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST,
-          bool ZSV, bool SYMT>
+          bool ZSV, bool SYMT, int BMA = BM>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, int8_t* s_x, float* s_scale,
                                           int8_t* s_zero, int* s_src, int* s_dst, float* s_xs, float* s_tw) {
   constexpr int NT = NW * 64;
@@ -265,7 +282,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   constexpr int WD = 2 * S;           // packed dwords per lane per (group, column block)
   constexpr int KC = KCG * GS;        // activation bytes per row per chunk
   constexpr int PITCH = KC + 32;      // LDS row pitch in bytes (see the layout note)
-  constexpr int BUF = BM * PITCH;     // bytes per LDS buffer
+  constexpr int BUF = BMA * PITCH;    // bytes per LDS buffer (BMA rows staged: the block and a tail)
   constexpr int UPR = KC / 16;        // 16-byte units per row and chunk
   constexpr int XU = (BMX * UPR + NT - 1) / NT;
   constexpr bool ZS_LDS = ZSG > 0;
@@ -314,7 +331,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // Padding rows read zeros (out-of-range offset) and are staged like the
   // others, which keeps the staging loops free of per-lane branches; their
   // results are never stored.
-  static_assert((BMX * UPR) % NT == 0, "staging units must divide evenly over the threads");
+  // The staging units divide evenly over the threads, except on bodies with a
+  // tail (144 rows): there the last round's surplus units read nothing (the
+  // out-of-range offset) and land in the 32-byte pads that end each staged
+  // row (two units a row), which the A fragments never read -- so the
+  // staging loops keep no per-lane branch.
+  constexpr int XSURPLUS = XU * NT - BMX * UPR;
+  static_assert(XSURPLUS == 0 || (PITCH - KC == 32 && XSURPLUS <= 2 * BMX),
+                "staging units must divide evenly over the threads or fit the row pads");
   uint32_t x_off[XU];
   int x_lds[XU];   // LDS byte offset within a buffer
   // reads the tile's source rows from LDS (s_src), so only after they are there
@@ -322,6 +346,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 #pragma unroll
     for (int j = 0; j < XU; ++j) {
       const int u = tid + j * NT;
+      if constexpr (XSURPLUS > 0) {
+        if (u >= BMX * UPR) {
+          const int v = u - BMX * UPR;
+          x_off[j] = kOOB;
+          x_lds[j] = (v >> 1) * PITCH + KC + 16 * (v & 1);
+          continue;
+        }
+      }
       const int q = u / UPR;
       const int cu = u - q * UPR;
       const int row = row_of_group<UPR>(q);
@@ -703,7 +735,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       if (!MG && u < z_units) *reinterpret_cast<u32x4*>(s_zero + 16 * u) = zq[j];
     }
   }
-  // STAGGER (8-wave 256-column tiles): half of the waves run the chunk
+  // STAGGER (full-height bodies of 8-wave 256-column tiles, with or without
+  // a tail): half of the waves run the chunk
   // interval in the opposite order, so that the CU's load bursts and compute
   // phases overlap: early waves loads(c+1), compute(c), store A(c+1); late
   // waves compute(c), store A(c+1) (loaded one interval earlier), loads(c+2) --
@@ -715,7 +748,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // its issue priority for its compute phase, so that a SIMD mate's loads and
   // staging fill the gaps rather than delay the MFMA chain (measured -0.75 %
   // over five interleaved runs).
-  constexpr bool STAGGER = NW == 8 && BMX == BM && CLAMP;
+  constexpr bool STAGGER = NW == 8 && BMX >= BM && CLAMP;
   if constexpr (STAGGER) {
     // one interval of chunk cc (ring parity d); LATE selects the order
     auto interval = [&](int cc, int d, auto late_tag) {
@@ -929,8 +962,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 
 // Entry of a 64/128-row tile (c: its block, rows, expert and columns):
 // routing rows and, with an LDS zero/scale block, the tile's symmetric
-// check, then the full-, half- or quarter-height body.
-template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST, bool ZSV>
+// check, then the full-, half- or quarter-height body -- or, for a tile that
+// takes the TAIL pairs of its expert's short last block (c.tail), the
+// full-height body extended by TAIL rows.
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST, bool ZSV,
+          int TAIL>
 __device__ __forceinline__ void prefill_tile_impl(const GemmArgs& a, TileCtx c, int8_t* s_x, float* s_scale,
                                                   int8_t* s_zero, int* s_src, int* s_dst, float* s_xs,
                                                   float* s_tw) {
@@ -959,10 +995,12 @@ __device__ __forceinline__ void prefill_tile_impl(const GemmArgs& a, TileCtx c, 
       }
     }
   }
-  if (tid < BM) {
-    int src, dst;
+  constexpr int BMA = BM + TAIL;
+  if (tid < BMA) {
+    int src = -1, dst = -1;
     float xsv = 0.f, twv = 1.f;
-    row_source<BM, ROUTED>(a, c, tid, src, dst);
+    if (tid < BM) row_source<BM, ROUTED>(a, c, tid, src, dst);
+    else if (c.tail >= 0) routed_slot(a, c.tail * BM + (tid - BM), src, dst);
     if (dst >= 0) row_scales<ROUTED, DEBUGP>(a, src, dst, xsv, twv);
     s_src[tid] = src;
     s_dst[tid] = dst;
@@ -978,22 +1016,29 @@ __device__ __forceinline__ void prefill_tile_impl(const GemmArgs& a, TileCtx c, 
   // symmetric tiles run the magic-number fold (SYMT)
   auto run = [&](auto symt_c) {
     constexpr bool SYMT = decltype(symt_c)::value;
+    if constexpr (TAIL > 0) {
+      if (rows > BM) {
+        gemm_body<BMA, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT, BMA>(a, c, s_x, s_scale, s_zero,
+                                                                                      s_src, s_dst, s_xs, s_tw);
+        return;
+      }
+    }
     if constexpr (BM >= 128 && NW == 8) {
       if (rows <= BM / 4) {
-        gemm_body<BM / 4, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero,
-                                                                                    s_src, s_dst, s_xs, s_tw);
+        gemm_body<BM / 4, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT, BMA>(a, c, s_x, s_scale, s_zero,
+                                                                                         s_src, s_dst, s_xs, s_tw);
         return;
       }
     }
     if constexpr (BM >= 64) {
       if (rows <= BM / 2) {
-        gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero,
-                                                                                    s_src, s_dst, s_xs, s_tw);
+        gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT, BMA>(a, c, s_x, s_scale, s_zero,
+                                                                                         s_src, s_dst, s_xs, s_tw);
         return;
       }
     }
-    gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT>(a, c, s_x, s_scale, s_zero, s_src,
-                                                                            s_dst, s_xs, s_tw);
+    gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT, BMA>(a, c, s_x, s_scale, s_zero, s_src,
+                                                                                 s_dst, s_xs, s_tw);
   };
   if constexpr (SYM_CHECK) {
     if (tsym) run(std::true_type{});
@@ -1065,23 +1110,30 @@ __device__ __forceinline__ void csr_block(int b, const int (&r0)[kCsrScanChunks]
 
 // ZSG > 0: zero points and scales come from an LDS copy of the tile's
 // block; the host launches this only when G <= ZSG (see zs_block_fits).
+//
+// TAIL > 0 (routed 128-row tiles): an expert's last block that holds at most
+// TAIL pairs is computed by the tile of the block before it, as TAIL extra
+// rows of that tile, so its weights are streamed once for both; the short
+// block's own tiles exit.
 template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST, bool ZSV,
-          int WAVES_PER_EU>
+          int WAVES_PER_EU, int TAIL = 0>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU)))
 void w4a8_gemm_kernel(const GemmArgs a) {
   constexpr int BN = NW * WN;
   constexpr int PITCH = KCG * GS + 32;
   constexpr bool ZS_LDS = ZSG > 0;
   constexpr bool ROUTED = RMODE != 0;
-  static_assert(BM % 16 == 0 && WN % 16 == 0 && GS % 64 == 0, "tile shape");
+  constexpr int BMA = BM + TAIL;   // rows staged: the block and a tail
+  static_assert(BM % 16 == 0 && WN % 16 == 0 && GS % 64 == 0 && TAIL % 16 == 0, "tile shape");
+  static_assert(TAIL == 0 || (ROUTED && BM >= 128 && NW == 8), "tails are taken by routed 8-wave 128-row tiles");
 
-  __shared__ __attribute__((aligned(16))) int8_t s_x[2 * BM * PITCH];
+  __shared__ __attribute__((aligned(16))) int8_t s_x[2 * BMA * PITCH];
   __shared__ __attribute__((aligned(16))) float s_scale[ZS_LDS ? BN * ZSG : 4];
   __shared__ __attribute__((aligned(16))) int8_t s_zero[ZS_LDS ? BN * ZSG : 16];
-  __shared__ int s_src[BM];
-  __shared__ int s_dst[BM];
-  __shared__ float s_xs[BM];
-  __shared__ float s_tw[BM];
+  __shared__ int s_src[BMA];
+  __shared__ int s_dst[BMA];
+  __shared__ float s_xs[BMA];
+  __shared__ float s_tw[BMA];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1116,7 +1168,7 @@ void w4a8_gemm_kernel(const GemmArgs a) {
     const int chunk_id = t / span;
     const int rem = t - chunk_id * span;
     nt = rem / a.R;
-    b = chunk_id * a.R + (rem - nt * a.R);
+    b = chunk_id * a.R + group_slot(rem - nt * a.R, nt, a.R);
     if (b >= nblocks) return;
     if constexpr (ROUTED) {
       e = a.expert_ids[b];
@@ -1130,10 +1182,18 @@ void w4a8_gemm_kernel(const GemmArgs a) {
     }
     if (e < 0) return;
   }
+  int tail = -1;
+  if constexpr (TAIL > 0) {
+    // block b is its expert's short last block, computed by block b - 1's tile
+    if (b > 0 && a.expert_ids[b - 1] == e && short_block<BM, TAIL>(a, b)) return;
+    // this tile computes block b + 1 as its tail
+    if (b + 1 < nblocks && a.expert_ids[b + 1] == e && short_block<BM, TAIL>(a, b + 1)) tail = b + 1;
+  }
 
   TileCtx c;
   c.e = e;
   c.blk = b;
+  c.tail = tail;
   c.row0 = row0;
   c.row1 = row1;
   c.tile_col0 = nt * BN;
@@ -1148,8 +1208,8 @@ void w4a8_gemm_kernel(const GemmArgs a) {
     gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, false>(a, c, s_x, s_scale, s_zero, s_src,
                                                                               s_dst, s_xs, s_tw);
   } else {
-    prefill_tile_impl<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV>(a, c, s_x, s_scale, s_zero, s_src,
-                                                                           s_dst, s_xs, s_tw);
+    prefill_tile_impl<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, TAIL>(a, c, s_x, s_scale, s_zero, s_src,
+                                                                                 s_dst, s_xs, s_tw);
   }
 }
 
@@ -1171,7 +1231,7 @@ static bool zs_block_fits(const GemmArgs& a, int BN, int ZSG) {
          reinterpret_cast<uintptr_t>(a.wz) % 16 == 0 && (a.ws == nullptr || reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
 }
 
-template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, int WPE>
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, int WPE, int TAIL = 0>
 static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   set_grid(a, max_blocks, NW * WN, R);
   // a column's zero points / scales of one window can be read as one aligned
@@ -1196,14 +1256,14 @@ static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   constexpr bool RUNS = ZSG == 0;   // vector zero/scale runs apply
   const dim3 grid(8 * a.per_xcd), block(NW * 64);
   if (CAN_FAST && a.G % (KCG * RD) == 0 && (ZSG > 0 || a.zs_vec))
-    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, CAN_FAST, RUNS, WPE>), grid,
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, CAN_FAST, RUNS, WPE, TAIL>), grid,
                        block, 0, s, a);
   else if (RUNS && a.zs_vec)
-    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, RUNS, WPE>), grid, block,
-                       0, s, a);
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, RUNS, WPE, TAIL>), grid,
+                       block, 0, s, a);
   else
-    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, false, WPE>), grid, block,
-                       0, s, a);
+    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, false, WPE, TAIL>), grid,
+                       block, 0, s, a);
   return hipGetLastError();
 }
 
@@ -1240,7 +1300,16 @@ hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, hipStrea
       // STAGGER; the 4-wave 256-row... body spilled at group size 256)
       if constexpr (GS >= 128) {
         // the tile's whole [256 x G] zero-point/scale block in LDS when G <= 64
-        // (80 KB beside the 72 KB of activation buffers: one tile per CU)
+        // (80 KB beside the 72 KB of activation buffers: one tile per CU).
+        // Routed, group size 128, G <= 56: a block of <= 16 pairs (an
+        // expert's short last block) rides on the tile before it as 16 extra
+        // rows (81 KB of activation buffers beside a 70 KB zero/scale block;
+        // at group size 256 that body spilled). DeepSeek-V3 up/gate M = 4096:
+        // 1534 -> 1425 us, every expert at 144 pairs 1782 -> 1443 us.
+        if constexpr (RMODE != 0 && GS == 128) {
+          if (zs_block_fits(a, 256, 56))
+            return launch_one<128, 32, 8, GS, K256, 2, 56, RMODE, DEBUGP, 2, 16>(a, max_blocks, c.R, s);
+        }
         if (zs_block_fits(a, 256, 64))
           return launch_one<128, 32, 8, GS, K256, 2, 64, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);
         return launch_one<128, 32, 8, GS, K256, 2, 0, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);

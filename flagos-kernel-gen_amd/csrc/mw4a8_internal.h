@@ -46,14 +46,30 @@ struct GemmArgs {
   int egroups;                // routed 64/128-row tiles in expert groups (expert_group_tile)
 };
 
+// Position of block slot i among the gs blocks that share column tile nt in
+// the tile list. One XCD's workgroups go to its four shader engines in turn
+// (the k-th workgroup of the XCD's run to a fixed engine, k mod 4 -- measured
+// with a placement probe; each engine then runs its own queue), so with the
+// same block order for every column tile an expert's full block and its
+// short last block alternate in the list and all the full blocks land on
+// the same engines. The order is rotated by the digit sum of nt in base gs
+// (a generalised Thue-Morse sequence), which spreads each block over the
+// positions mod 4 (for gs = 2 and 4: evenly over every 4 column tiles).
+__host__ __device__ inline int group_slot(int i, int nt, int gs) {
+  if (gs <= 1) return i;
+  int r = 0;
+  for (int v = nt; v > 0; v /= gs) r += v % gs;
+  return (i + r) % gs;
+}
+
 // Expert-grouped tile order of a routed launch. The row blocks of one
 // expert's run (expert_ids ascends over the blocks, as moe_align lays them
 // out) form groups of up to R blocks counted from the run's first block; a
-// group's tiles take the column tiles in turn, its blocks innermost, so the
-// tiles that share one column tile of one expert's weights are adjacent in
-// the list and run at the same time on one XCD. Every block keeps n_tiles
-// tiles inside its group's range, so block t / n_tiles lies in the group of
-// tile t. Writes block b, column tile nt and expert e of tile t in
+// group's tiles take the column tiles in turn, its blocks innermost (in the
+// rotated order of group_slot), so the tiles that share one column tile of
+// one expert's weights are adjacent in the list and run at the same time on
+// one XCD. Every block keeps n_tiles tiles inside its group's range, so
+// block t / n_tiles lies in the group of tile t. Writes block b, column tile nt and expert e of tile t in
 // [0, nblocks * n_tiles); false when the block has no expert in [0, E).
 // The run start is found by a binary search, which needs ascending
 // expert_ids: on a table that is not sorted the returned group may not hold
@@ -77,7 +93,7 @@ __host__ __device__ inline bool expert_group_tile(int t, int n_tiles, int R, int
   while (gs < R && g0 + gs < nblocks && expert_ids[g0 + gs] == e) ++gs;
   const int local = t - g0 * n_tiles;
   nt = local / gs;
-  b = g0 + (local - nt * gs);
+  b = g0 + group_slot(local - nt * gs, nt, gs);
   return nt < n_tiles;
 }
 

@@ -160,6 +160,33 @@ def test_routed_partials_bit_exact(pkg, dev, bm, zero):
     assert_close(out, ref_out, N, f"routed partials bm={bm} {zero}")
 
 
+@pytest.mark.parametrize("zero", ["symmetric", "uint4"])
+def test_routed_tail_blocks_bit_exact(pkg, dev, zero):
+    """An expert's short last block (at most 16 pairs) is computed by the
+    128-row tile of the block before it, as 16 extra rows, and its own tiles
+    exit. Per-expert loads of 144 (a 16-row tail), 145 (17 rows: its own
+    quarter-height tile), 272 (two full blocks, the second with a tail), 128,
+    16 (a short block with no block before it) and 1, at the DeepSeek-V3 slice
+    (G = 56: the tail kernel). Every partial of every pair bit-exact (a pair
+    no tile computed would read zero), the bf16 output within the
+    tolerance."""
+    loads = [144, 145, 272, 128, 16, 1]
+    N, K, gs = 2048, 7168, 128
+    print(f"[tail blocks] zero={zero}", flush=True)
+    x_q, x_scale, w_q4, w_scale, w_zero, ids, tw = _routed_partials_case(pkg, loads, N, K, gs, zero, 71)
+    out, part = pkg.w4a8_fused_moe_partials(*[t.to(dev) for t in (x_q, x_scale, w_q4, w_scale, w_zero, ids, tw)],
+                                            group_size=gs, block_m=128)
+    part = part.cpu()
+    flat = ids.reshape(-1)
+    for e in range(len(loads)):
+        pe = (flat == e).nonzero().reshape(-1)
+        w_e = task1_ref.fold_zero(task1_ref.unpack_int4(w_q4[e]), w_zero[e], gs)
+        ref = task1_ref.group_partials(x_q[pe], w_e, gs).to(torch.int32)
+        assert torch.equal(part[pe], ref), f"expert {e}: {int((part[pe] != ref).sum())} partials differ"
+    ref_out = task1_ref.fused_moe_ref(x_q, x_scale, w_q4, w_scale, w_zero, ids, tw, gs)
+    assert_close(out, ref_out, N, f"tail blocks {zero}")
+
+
 @pytest.mark.parametrize("bm", [16, 64, 128])
 def test_routed_partials_repacked_bit_exact(pkg, dev, bm):
     """Same on weights in the repacked MFMA order (symmetric zero points)."""
