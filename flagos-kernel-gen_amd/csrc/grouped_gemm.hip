@@ -76,9 +76,11 @@ TileConfig select_tiles(int rows, int touched_experts, int N, int K, int group_s
   // a small problem keeps the 16-row tiles' larger grid (64-row tiles span
   // 128 columns: fewer than 256 tiles leave CUs idle)
   if (per_expert <= 32 && (int64_t)ne * ((N + 127) / 128) < 256) return tiles_for_block_m(16, group_size);
-  // 128-row tiles pay off only over a long K loop (measured on MI355X:
-  // K = 7168 prefers 128 rows, K = 2048 prefers 64)
-  if (per_expert <= 64 || K < 4096) return tiles_for_block_m(64, group_size);
+  // 128-row tiles over more than 64 rows an expert (measured on MI355X with
+  // the tail rows and the rotated block order: DeepSeek-V3 up/gate K = 7168
+  // 1391 vs 1950 us with 64 rows, down K = 2048 839 vs 961 us, Qwen3 K = 2048
+  // 112 either way); shorter K loops keep the 64-row tiles
+  if (per_expert <= 64 || K < 2048) return tiles_for_block_m(64, group_size);
   return tiles_for_block_m(128, group_size);
 }
 

@@ -54,9 +54,11 @@ def test_sizes_and_tile_selection(pkg):
     assert pkg.select_block_m(384 * 8, 256, 7168, 2048, 128) == 64     # DSv3 down M=384: 12 rows
     assert pkg.select_block_m(256 * 8, 128, 1536, 2048, 128) == 64     # Qwen3 M=256: 16 rows
     assert pkg.select_block_m(1024 * 8, 256, 4096, 7168, 128) == 64    # DSv3 up M=1024: 32 rows
-    # long expert row lists: 128-row tiles for a long K loop, 64 for a short one
-    assert pkg.select_block_m(32768, 256, 7168, 2048, 128) == 64
-    assert pkg.select_block_m(16384, 128, 1536, 2048, 128) == 64
+    # long expert row lists: 128-row tiles from K = 2048 (DSv3 down M=4096,
+    # Qwen3 M=2048), 64 below
+    assert pkg.select_block_m(32768, 256, 7168, 2048, 128) == 128
+    assert pkg.select_block_m(16384, 128, 1536, 2048, 128) == 128
+    assert pkg.select_block_m(16384, 128, 1536, 1024, 128) == 64
 
 
 def test_c_abi_rejects_bad_arguments_without_device_work(pkg):
