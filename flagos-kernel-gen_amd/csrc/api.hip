@@ -557,6 +557,19 @@ int mw4a8_host_selftest(void) {
     }
     for (int i = 0; i < nblocks * n_tiles; ++i) bad += seen[i] != 1;
   }
+  // the rotated block order within a column tile (group_slot) is a
+  // permutation of the group's slots for every group size and column tile,
+  // as both tile orders (expert groups and fixed row-block groups) need
+  for (int gs = 1; gs <= 16; ++gs)
+    for (int nt = 0; nt < 512; ++nt) {
+      uint32_t hit = 0;
+      for (int i = 0; i < gs; ++i) {
+        const int j = group_slot(i, nt, gs);
+        bad += j < 0 || j >= gs;
+        if (j >= 0 && j < gs) hit |= 1u << j;
+      }
+      bad += hit != (gs == 32 ? ~0u : (1u << gs) - 1u);
+    }
   // an expert_ids table that is not ascending (not what moe_align writes):
   // the grouped order may skip tiles, but never pairs a block with another
   // expert's weights
