@@ -187,6 +187,28 @@ def test_routed_tail_blocks_bit_exact(pkg, dev, zero):
     assert_close(out, ref_out, N, f"tail blocks {zero}")
 
 
+@pytest.mark.parametrize("N,K,zero", [(200, 2048, "full"), (1400, 2048, "symmetric"), (256, 4096, "uint4")])
+def test_routed_tail_blocks_odd_shapes(pkg, dev, N, K, zero):
+    """Tail rows on column counts that leave a partial (or lone) 256-column
+    tile and at K = 2048, the shortest K that takes 128-row tiles: loads of
+    144, 130 (a 2-row tail), 17, 272 and 16. Every partial bit-exact."""
+    loads = [144, 130, 17, 272, 16]
+    gs = 128
+    print(f"[tail odd] N={N} K={K} zero={zero}", flush=True)
+    x_q, x_scale, w_q4, w_scale, w_zero, ids, tw = _routed_partials_case(pkg, loads, N, K, gs, zero, 73 + N)
+    out, part = pkg.w4a8_fused_moe_partials(*[t.to(dev) for t in (x_q, x_scale, w_q4, w_scale, w_zero, ids, tw)],
+                                            group_size=gs, block_m=128)
+    part = part.cpu()
+    flat = ids.reshape(-1)
+    for e in range(len(loads)):
+        pe = (flat == e).nonzero().reshape(-1)
+        w_e = task1_ref.fold_zero(task1_ref.unpack_int4(w_q4[e]), w_zero[e], gs)
+        ref = task1_ref.group_partials(x_q[pe], w_e, gs).to(torch.int32)
+        assert torch.equal(part[pe], ref), f"expert {e}: {int((part[pe] != ref).sum())} partials differ"
+    ref_out = task1_ref.fused_moe_ref(x_q, x_scale, w_q4, w_scale, w_zero, ids, tw, gs)
+    assert_close(out, ref_out, N, f"tail odd N={N} K={K} {zero}")
+
+
 @pytest.mark.parametrize("bm", [16, 64, 128])
 def test_routed_partials_repacked_bit_exact(pkg, dev, bm):
     """Same on weights in the repacked MFMA order (symmetric zero points)."""
