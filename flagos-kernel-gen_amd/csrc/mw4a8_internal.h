@@ -69,8 +69,9 @@ __host__ __device__ inline int group_slot(int i, int nt, int gs) {
 // rotated order of group_slot), so the tiles that share one column tile of
 // one expert's weights are adjacent in the list and run at the same time on
 // one XCD. Every block keeps n_tiles tiles inside its group's range, so
-// block t / n_tiles lies in the group of tile t. Writes block b, column tile nt and expert e of tile t in
-// [0, nblocks * n_tiles); false when the block has no expert in [0, E).
+// block t / n_tiles lies in the group of tile t. Writes block b, column
+// tile nt and expert e of tile t in [0, nblocks * n_tiles); false when the
+// block has no expert in [0, E).
 // The run start is found by a binary search, which needs ascending
 // expert_ids: on a table that is not sorted the returned group may not hold
 // block t / n_tiles, so every block of the group is checked to belong to e
