@@ -136,9 +136,12 @@ int mw4a8_moe_align(const int32_t* topk_ids, int num_pairs, int E, int block_m, 
  *  same block_m, out [M * topk, N] bf16 (stride ldo). Rows of pairs that are
  *  not routed are left untouched. block_m in {16, 32, 64, 128}.
  *  Routing metadata built by other means must have moe_align's form: each
- *  expert's pairs in consecutive blocks and expert_ids non-decreasing over
- *  the num_post_pad / block_m used blocks (blocks of an out-of-order table
- *  may be skipped; none is computed with another expert's weights).
+ *  expert's pairs in consecutive blocks, filling each block from its first
+ *  slot (padding only after an expert's last pair), and expert_ids
+ *  non-decreasing over the num_post_pad / block_m used blocks (blocks of an
+ *  out-of-order table may be skipped; none is computed with another
+ *  expert's weights). With block_m = 128 an expert's last block of at most
+ *  16 pairs is computed together with the block before it.
  */
 int mw4a8_fused_moe(const int8_t* x_q, int64_t ldx, const float* x_scale, const uint8_t* w_q4,
                     const float* w_scale, const int8_t* w_zero, const int32_t* sorted_ids,
