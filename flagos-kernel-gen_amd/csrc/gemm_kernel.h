@@ -46,6 +46,7 @@
 // This header holds the kernel template and its launch helpers; each
 // gemm_*.hip file instantiates dispatch_bm for one row source.
 #pragma once
+#include <mutex>
 #include <type_traits>
 
 #include "mw4a8_internal.h"
@@ -75,6 +76,16 @@ constexpr int kRsrcFlags = 0x00020000;   // raw buffer, 32-bit data format
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcFlags);
+}
+
+// The thread's index, read so that the compiler cannot reuse an earlier
+// read: in a persistent launch every value a tile body derives from it is
+// then computed inside the tile loop rather than hoisted out of it and kept
+// live across the whole loop (which spilled the 128-row bodies).
+__device__ __forceinline__ int opaque_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
 }
 
 // KCG consecutive int8 zero points at byte offset `off` (KCG-aligned), kept
@@ -245,6 +256,24 @@ __device__ __forceinline__ void row_scales(const GemmArgs& a, int src, int dst, 
   if constexpr (ROUTED) twv = a.tw ? a.tw[dst] : 1.f;
 }
 
+// Work a persistent launch fits into a tile body (see the persistent
+// kernel): before_barrier() runs once the body has requested its first
+// chunk's loads (before the body's first barrier), before_epilogue() once
+// the K loop is done, before_stores() in the epilogue before its first
+// global store (values loaded in before_epilogue() are consumed there:
+// waiting for a load issued before the output stores, whose number varies
+// by row, waits for all of them), and the row factors ep_xs / ep_tw
+// (activation scale, routing weight of row threadIdx.x) go to LDS just
+// before the epilogue, their loads having run during the K loop. A plain
+// launch has no hooks.
+struct NoHooks {
+  static constexpr bool kActive = false;
+  float ep_xs = 0.f, ep_tw = 1.f;
+  __device__ __forceinline__ void before_barrier() {}
+  __device__ __forceinline__ void before_epilogue() {}
+  __device__ __forceinline__ void before_stores() {}
+};
+
 // Main K loop and epilogue for the first BMX rows of a tile (BMX <= BM).
 //
 // RD: weight-register ring depth. The weights (and, unless ZS_LDS, the zero
@@ -271,9 +300,10 @@ __device__ __forceinline__ void row_scales(const GemmArgs& a, int src, int dst, 
 //     join, and waited there for every outstanding load, which serialized
 //     the prefetch with the compute.
 template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST,
-          bool ZSV, bool SYMT, int BMA = BM>
+          bool ZSV, bool SYMT, int BMA = BM, class Hooks = NoHooks>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, int8_t* s_x, float* s_scale,
-                                          int8_t* s_zero, int* s_src, int* s_dst, float* s_xs, float* s_tw) {
+                                          int8_t* s_zero, int* s_src, int* s_dst, float* s_xs, float* s_tw,
+                                          Hooks* hk = nullptr) {
   constexpr int NT = NW * 64;
   constexpr int MB = BMX / 16;        // 16-row blocks computed
   constexpr int NB = WN / 16;         // 16-column blocks per wave
@@ -295,7 +325,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // exact int32 group partial (decoded from its chain, see fold) to a.dbg.
   constexpr bool MG = SYMT && ZS_LDS;
 
-  const int tid = threadIdx.x;
+  const int tid = opaque_tid();
   const int lane = tid & 63;
   const int jl = lane & 15;   // row (A) / column (B) within a 16-block
   const int kb = lane >> 4;   // K slot group of the MFMA operands
@@ -342,7 +372,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   uint32_t x_off[XU];
   int x_lds[XU];   // LDS byte offset within a buffer
   // reads the tile's source rows from LDS (s_src), so only after they are there
-  auto init_x = [&]() {
+  auto init_x = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < XU; ++j) {
       const int u = tid + j * NT;
@@ -405,13 +435,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // the chunk's K offset moves the descriptor (scalar work) rather than going
   // into the unchecked scalar offset: units past K in a partial last chunk of
   // the tensor's last row then read as zero instead of past its end
-  auto load_x = [&](int ch, int slot) {
+  auto load_x = [&](int ch, int slot) __attribute__((always_inline)) {
     const uint32_t base = (uint32_t)(ch * KC);
     const __amdgpu_buffer_rsrc_t r = make_rsrc(a.x + base, a.x_bytes - base);
 #pragma unroll
     for (int j = 0; j < XU; ++j) xr[slot][j] = __builtin_amdgcn_raw_buffer_load_b128(r, x_off[j], 0, 0);
   };
-  auto store_x = [&](int buf, int slot) {
+  auto store_x = [&](int buf, int slot) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < XU; ++j) {
       const u32x4 v = xr[slot][j];
@@ -441,7 +471,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     uint32_t zr[NB][(KW + 3) / 4];
     float s[KW][NB];
   };
-  auto load_zs = [&](int win, ZsWin& d) {
+  auto load_zs = [&](int win, ZsWin& d) __attribute__((always_inline)) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const uint32_t zo = zs_off[nb] + (uint32_t)(win * KW);
@@ -449,7 +479,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       load_scale_run<KW, NB>(s_rsrc, zo * 4u, d.s, nb);
     }
   };
-  auto load_w = [&](int ch, WChunk& d) {
+  auto load_w = [&](int ch, WChunk& d) __attribute__((always_inline)) {
 #pragma unroll
     for (int g = 0; g < KCG; ++g) {
       const uint32_t gg = (uint32_t)(ch * KCG + g);
@@ -506,7 +536,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   float bias[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) bias[nb] = 0.f;
-  auto rebase = [&]() {
+  auto rebase = [&]() __attribute__((always_inline)) {
     if constexpr (MG) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
@@ -518,7 +548,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       for (int nb = 0; nb < NB; ++nb) bias[nb] = 0.f;
     }
   };
-  auto compute = [&](int ch, const int8_t* xb, const WChunk& wc, const ZsWin& zw, int dd) {
+  auto compute = [&](int ch, const int8_t* xb, const WChunk& wc, const ZsWin& zw, int dd) __attribute__((always_inline)) {
 #pragma unroll
     for (int g = 0; g < KCG; ++g) {
       const int gg = ch * KCG + g;
@@ -604,11 +634,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         // mb's MFMAs are issued, so neither the LDS latency nor the MFMA
         // result latency sits on the issue path.
         const int8_t* xg = xb + jl * PITCH + g * GS + kb * 16;
-        auto read_a = [&](int mb, i32x4 (&av)[S]) {
+        auto read_a = [&](int mb, i32x4 (&av)[S]) __attribute__((always_inline)) {
 #pragma unroll
           for (int s = 0; s < S; ++s) av[s] = *reinterpret_cast<const i32x4*>(xg + mb * 16 * PITCH + 64 * s);
         };
-        auto fold = [&](int mb, const i32x4 (&part)[NB]) {
+        auto fold = [&](int mb, const i32x4 (&part)[NB]) __attribute__((always_inline)) {
           if constexpr (DEBUGP) {
             // the exact partial from the chain's value: minus the seed on
             // magic-seeded chains, / 16 (exact) after the symmetric unpack
@@ -711,6 +741,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     load_x(0, 0);
 #pragma unroll
     for (int d = 0; d < RD - 1; ++d) load_w(min(d, last_chunk), ring[d]);
+    if constexpr (Hooks::kActive) hk->before_barrier();
   }
   if constexpr (ZS_LDS) {
     // visible to all waves after the first barrier of the loop; a symmetric
@@ -751,7 +782,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   constexpr bool STAGGER = NW == 8 && BMX >= BM && CLAMP;
   if constexpr (STAGGER) {
     // one interval of chunk cc (ring parity d); LATE selects the order
-    auto interval = [&](int cc, int d, auto late_tag) {
+    auto interval = [&](int cc, int d, auto late_tag) __attribute__((always_inline)) {
       constexpr bool LATE = decltype(late_tag)::value;
       if constexpr (!ZS_LDS && ZSV) {
         if (d % ZW == 0) {
@@ -782,7 +813,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     // condition, the loop header had a predecessor that issued no loads after
     // the current weights, and the wait-count merge there made every other
     // compute phase wait for the loads issued just before the barrier.
-    auto run_loop = [&](auto late_tag) {
+    auto run_loop = [&](auto late_tag) __attribute__((always_inline)) {
       int ch = 0;
       for (; ch + RD <= c.nchunks; ch += RD) {
 #pragma unroll
@@ -816,7 +847,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     // The main loop runs while every such request exists, so it holds no
     // conditional load (a join after one makes the wait-count merge assume
     // the fewest loads in flight); the last chunks follow in a guarded tail.
-    auto step = [&](int cc, int d, bool load_next) {
+    auto step = [&](int cc, int d, bool load_next) __attribute__((always_inline)) {
       store_x(cc & 1, d);
       __syncthreads();
       const int nx = cc + RD - 1, slot = (d + RD - 1) % RD;
@@ -843,7 +874,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     }
   }
   if constexpr (!STAGGER && !XDEEP) {
-    auto step = [&](int cc, int d) {
+    auto step = [&](int cc, int d) __attribute__((always_inline)) {
       store_x(cc & 1, 0);
       __syncthreads();
       if constexpr (!ZS_LDS && ZSV) {
@@ -878,6 +909,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     }
   }
 
+  if constexpr (Hooks::kActive) {
+    hk->before_epilogue();
+    // (read by the epilogue only, after its first barrier)
+    const int r = opaque_tid();
+    if (r < BMA) {
+      s_xs[r] = hk->ep_xs;
+      s_tw[r] = hk->ep_tw;
+    }
+  }
   // (the reference-layout debug export passes no output)
   if (!DEBUGP || a.out != nullptr) {
     if constexpr (XDEEP) {
@@ -926,6 +966,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
             }
           }
         __syncthreads();
+        if constexpr (Hooks::kActive) hk->before_stores();
         static_assert((BMX * SEG) % NT == 0, "output rounds");
 #pragma unroll
         for (int i = 0; i < BMX * SEG / NT; ++i) {
@@ -940,6 +981,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       }
     }
     if (!stored) {
+      if constexpr (Hooks::kActive) {
+        __syncthreads();   // the row factors just stored
+        hk->before_stores();
+      }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -957,95 +1002,174 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
           }
         }
     }
+  } else if constexpr (Hooks::kActive) {
+    hk->before_stores();
   }
 }
 
-// Entry of a 64/128-row tile (c: its block, rows, expert and columns):
-// routing rows and, with an LDS zero/scale block, the tile's symmetric
-// check, then the full-, half- or quarter-height body -- or, for a tile that
+// Routing rows of a 64/128-row tile, loaded ahead of their use: this
+// thread's sorted_ids entry (routed tiles; row tid of the block, or of the
+// tail for tid >= BM) and its share of the tile's [BN x G] zero-point block
+// for the symmetric check (tiles with an LDS zero/scale block).
+template <int ZCU>
+struct RowsAhead {
+  int sid;
+  u32x4 zq[ZCU];
+};
+
+template <int BN, int NT, int ZSG>
+__host__ __device__ constexpr int zero_check_units() {
+  return ZSG > 0 ? (BN * ZSG / 16 + NT - 1) / NT : 1;
+}
+
+template <int BM, int BN, int NT, int ZSG, int TAIL, bool ROUTED>
+__device__ __forceinline__ void prefill_rows_issue(const GemmArgs& a, const TileCtx& c,
+                                                   RowsAhead<zero_check_units<BN, NT, ZSG>()>& p) {
+  constexpr int ZCU = zero_check_units<BN, NT, ZSG>();
+  const int tid = opaque_tid();
+  p.sid = -1;
+  if constexpr (ROUTED) {
+    if (tid < BM) p.sid = a.sorted_ids[c.blk * BM + tid];
+    else if (tid < BM + TAIL && c.tail >= 0) p.sid = a.sorted_ids[c.tail * BM + (tid - BM)];
+  }
+  if constexpr (ZSG > 0) {
+    const __amdgpu_buffer_rsrc_t zr = make_rsrc(a.wz + (int64_t)c.e * a.N * a.G, (uint32_t)(a.N * a.G));
+    const int z_units = BN * a.G / 16;
+#pragma unroll
+    for (int j = 0; j < ZCU; ++j) {
+      const int u = tid + j * NT;
+      p.zq[j] = u32x4{0u, 0u, 0u, 0u};
+      if (u < z_units) p.zq[j] = __builtin_amdgcn_raw_buffer_load_b128(zr, (uint32_t)(c.tile_col0 * a.G) + u * 16u, 0, 0);
+    }
+  }
+}
+
+// This thread's row of the tile (src: activation row, dst: output row,
+// -1 for padding) from its sorted_ids entry, and whether its share of the
+// zero-point block is all 8 (columns past N read zero: not symmetric).
+template <int BM, int BN, int NT, int ZSG, int TAIL, bool ROUTED>
+__device__ __forceinline__ void prefill_rows_settle(const GemmArgs& a, const TileCtx& c,
+                                                    const RowsAhead<zero_check_units<BN, NT, ZSG>()>& p, int& zok,
+                                                    int& src, int& dst) {
+  constexpr int ZCU = zero_check_units<BN, NT, ZSG>();
+  const int tid = opaque_tid();
+  zok = 1;
+  if constexpr (ZSG > 0) {
+    const int z_units = BN * a.G / 16;
+#pragma unroll
+    for (int j = 0; j < ZCU; ++j) {
+      const u32x4 q = p.zq[j];
+      if (tid + j * NT < z_units)
+        zok &= (q.x == 0x08080808u) & (q.y == 0x08080808u) & (q.z == 0x08080808u) & (q.w == 0x08080808u);
+    }
+  }
+  src = dst = -1;
+  if (tid < BM + TAIL) {
+    if constexpr (ROUTED) {
+      if (p.sid >= 0 && p.sid < a.num_pairs) {
+        src = p.sid / a.topk;
+        dst = p.sid;
+      }
+    } else {
+      if (tid < BM) row_source<BM, false>(a, c, tid, src, dst);
+    }
+  }
+}
+
+// The rows into LDS (s_src, s_dst; s_rows raised to the last row holding
+// data, from zero) and this row's epilogue factors requested into xsv / twv.
+template <int BM, int TAIL, bool ROUTED, bool DEBUGP>
+__device__ __forceinline__ void prefill_rows_place(const GemmArgs& a, int src, int dst, int* s_src, int* s_dst,
+                                                   int* s_rows, float& xsv, float& twv) {
+  const int tid = opaque_tid();
+  xsv = 0.f;
+  twv = 1.f;
+  if (tid < BM + TAIL) {
+    if (dst >= 0) row_scales<ROUTED, DEBUGP>(a, src, dst, xsv, twv);
+    s_src[tid] = src;
+    s_dst[tid] = dst;
+    if (dst >= 0) atomicMax(s_rows, tid + 1);
+  }
+}
+
+// Body of a 64/128-row tile whose rows are in LDS (c.rows: rows holding
+// data): the full-, half- or quarter-height body -- or, for a tile that
 // takes the TAIL pairs of its expert's short last block (c.tail), the
-// full-height body extended by TAIL rows.
+// full-height body extended by TAIL rows; symmetric tiles (tsym) run the
+// magic-number fold (SYMT).
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST, bool ZSV,
+          int TAIL, class Hooks = NoHooks>
+__device__ __forceinline__ void prefill_run(const GemmArgs& a, const TileCtx& c, bool tsym, int8_t* s_x,
+                                            float* s_scale, int8_t* s_zero, int* s_src, int* s_dst, float* s_xs,
+                                            float* s_tw, Hooks* hk = nullptr) {
+  constexpr int BMA = BM + TAIL;
+  const int rows = c.rows;
+  auto run = [&](auto symt_c) __attribute__((always_inline)) {
+    constexpr bool SYMT = decltype(symt_c)::value;
+    if constexpr (TAIL > 0) {
+      if (rows > BM) {
+        gemm_body<BMA, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT, BMA, Hooks>(
+            a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs, s_tw, hk);
+        return;
+      }
+    }
+    // tiles whose valid rows fit in the top quarter (8-wave 128-row tiles:
+    // the second block of most DeepSeek-V3 experts) or half
+    if constexpr (BM >= 128 && NW == 8) {
+      if (rows <= BM / 4) {
+        gemm_body<BM / 4, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT, BMA, Hooks>(
+            a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs, s_tw, hk);
+        return;
+      }
+    }
+    if constexpr (BM >= 64) {
+      if (rows <= BM / 2) {
+        gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT, BMA, Hooks>(
+            a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs, s_tw, hk);
+        return;
+      }
+    }
+    gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT, BMA, Hooks>(
+        a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs, s_tw, hk);
+  };
+  if constexpr (ZSG > 0) {
+    if (tsym) run(std::true_type{});
+    else run(std::false_type{});
+  } else {
+    run(std::false_type{});
+  }
+}
+
+// Entry of a 64/128-row tile of a plain launch (c: its block, expert and
+// columns): routing rows and, with an LDS zero/scale block, the tile's
+// symmetric check (loads issued together, checked at one barrier), then
+// the body.
 template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST, bool ZSV,
           int TAIL>
 __device__ __forceinline__ void prefill_tile_impl(const GemmArgs& a, TileCtx c, int8_t* s_x, float* s_scale,
                                                   int8_t* s_zero, int* s_src, int* s_dst, float* s_xs,
                                                   float* s_tw) {
   constexpr int BN = NW * WN;
+  constexpr int NT = NW * 64;
   constexpr bool ROUTED = RMODE != 0;
-  const int tid = threadIdx.x;
+  const int tid = opaque_tid();
   __shared__ int s_rows;   // rows of the tile holding data
   if (tid == 0) s_rows = 0;
   __syncthreads();
-  // Tiles with an LDS zero/scale block: is every zero point of the tile's
-  // [BN x G] block 8 (symmetric int4)? The loads go out with the routing
-  // rows' and are checked at the same barrier. Columns past N read zero
-  // (not symmetric).
-  constexpr bool SYM_CHECK = ZSG > 0;
-  constexpr int ZCU = SYM_CHECK ? (BN * ZSG / 16 + NW * 64 - 1) / (NW * 64) : 1;
-  int zok = 1;
-  if constexpr (SYM_CHECK) {
-    const __amdgpu_buffer_rsrc_t zr = make_rsrc(a.wz + (int64_t)c.e * a.N * a.G, (uint32_t)(a.N * a.G));
-    const int z_units = BN * a.G / 16;
-#pragma unroll
-    for (int j = 0; j < ZCU; ++j) {
-      const int u = tid + j * NW * 64;
-      if (u < z_units) {
-        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(zr, (uint32_t)(c.tile_col0 * a.G) + u * 16u, 0, 0);
-        zok &= (q.x == 0x08080808u) & (q.y == 0x08080808u) & (q.z == 0x08080808u) & (q.w == 0x08080808u);
-      }
-    }
-  }
-  constexpr int BMA = BM + TAIL;
-  if (tid < BMA) {
-    int src = -1, dst = -1;
-    float xsv = 0.f, twv = 1.f;
-    if (tid < BM) row_source<BM, ROUTED>(a, c, tid, src, dst);
-    else if (c.tail >= 0) routed_slot(a, c.tail * BM + (tid - BM), src, dst);
-    if (dst >= 0) row_scales<ROUTED, DEBUGP>(a, src, dst, xsv, twv);
-    s_src[tid] = src;
-    s_dst[tid] = dst;
+  RowsAhead<zero_check_units<BN, NT, ZSG>()> p;
+  prefill_rows_issue<BM, BN, NT, ZSG, TAIL, ROUTED>(a, c, p);
+  int zok, src, dst;
+  prefill_rows_settle<BM, BN, NT, ZSG, TAIL, ROUTED>(a, c, p, zok, src, dst);
+  float xsv, twv;
+  prefill_rows_place<BM, TAIL, ROUTED, DEBUGP>(a, src, dst, s_src, s_dst, &s_rows, xsv, twv);
+  if (tid < BM + TAIL) {
     s_xs[tid] = xsv;
     s_tw[tid] = twv;
-    if (dst >= 0) atomicMax(&s_rows, tid + 1);
   }
-  const bool tsym = SYM_CHECK ? __syncthreads_and(zok) != 0 : (__syncthreads(), false);
-  const int rows = __builtin_amdgcn_readfirstlane(s_rows);
-  c.rows = rows;
-  // tiles whose valid rows fit in the top quarter (8-wave 128-row tiles: the
-  // second block of most DeepSeek-V3 experts) or half run a shorter body;
-  // symmetric tiles run the magic-number fold (SYMT)
-  auto run = [&](auto symt_c) {
-    constexpr bool SYMT = decltype(symt_c)::value;
-    if constexpr (TAIL > 0) {
-      if (rows > BM) {
-        gemm_body<BMA, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT, BMA>(a, c, s_x, s_scale, s_zero,
-                                                                                      s_src, s_dst, s_xs, s_tw);
-        return;
-      }
-    }
-    if constexpr (BM >= 128 && NW == 8) {
-      if (rows <= BM / 4) {
-        gemm_body<BM / 4, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT, BMA>(a, c, s_x, s_scale, s_zero,
-                                                                                         s_src, s_dst, s_xs, s_tw);
-        return;
-      }
-    }
-    if constexpr (BM >= 64) {
-      if (rows <= BM / 2) {
-        gemm_body<BM / 2, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT, BMA>(a, c, s_x, s_scale, s_zero,
-                                                                                         s_src, s_dst, s_xs, s_tw);
-        return;
-      }
-    }
-    gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, SYMT, BMA>(a, c, s_x, s_scale, s_zero, s_src,
-                                                                                 s_dst, s_xs, s_tw);
-  };
-  if constexpr (SYM_CHECK) {
-    if (tsym) run(std::true_type{});
-    else run(std::false_type{});
-  } else {
-    run(std::false_type{});
-  }
+  const bool tsym = ZSG > 0 ? __syncthreads_and(zok) != 0 : (__syncthreads(), false);
+  c.rows = __builtin_amdgcn_readfirstlane(s_rows);
+  prefill_run<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, TAIL>(a, c, tsym, s_x, s_scale, s_zero, s_src,
+                                                                          s_dst, s_xs, s_tw);
 }
 
 // Reference layout without a block table: the row blocks of expert e are
@@ -1108,6 +1232,81 @@ __device__ __forceinline__ void csr_block(int b, const int (&r0)[kCsrScanChunks]
   }
 }
 
+// Inclusive sum / max over the workgroup's threads in thread order; total
+// receives the whole workgroup's sum / max. Every thread calls it; s_tmp
+// holds NW ints.
+template <int NW>
+__device__ __forceinline__ int block_scan_add(int v, int* s_tmp, int& total) {
+  const int tid = opaque_tid(), lane = tid & 63, w = tid >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  if (lane == 63) s_tmp[w] = v;
+  __syncthreads();
+  int pre = 0, tot = 0;
+#pragma unroll
+  for (int k = 0; k < NW; ++k) {
+    const int y = s_tmp[k];
+    if (k < w) pre += y;
+    tot += y;
+  }
+  __syncthreads();
+  total = __builtin_amdgcn_readfirstlane(tot);
+  return pre + v;
+}
+
+template <int NW>
+__device__ __forceinline__ int block_scan_max(int v, int* s_tmp, int& top) {
+  const int tid = opaque_tid(), lane = tid & 63, w = tid >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d, 64);
+    if (lane >= d) v = max(v, o);
+  }
+  if (lane == 63) s_tmp[w] = v;
+  __syncthreads();
+  int pre = -1, tot = -1;
+#pragma unroll
+  for (int k = 0; k < NW; ++k) {
+    const int y = s_tmp[k];
+    if (k < w) pre = max(pre, y);
+    tot = max(tot, y);
+  }
+  __syncthreads();
+  top = __builtin_amdgcn_readfirstlane(tot);
+  return max(pre, v);
+}
+
+// Hooks of a persistent launch's tile body (see NoHooks).
+template <class A, class B, class C>
+struct TileHooks {
+  static constexpr bool kActive = true;
+  A& before;
+  B& after;
+  C& settle;
+  float ep_xs, ep_tw;
+  __device__ __forceinline__ void before_barrier() { before(); }
+  __device__ __forceinline__ void before_epilogue() { after(); }
+  __device__ __forceinline__ void before_stores() { settle(); }
+};
+
+// Row blocks the compact block table of a persistent launch holds in the LDS
+// left beside a tile's buffers (6 bytes a block; at most 1024).
+__host__ __device__ constexpr int compact_blocks(int BMA, int PITCH, int BN, int ZSG) {
+  return (163840 - 512 - (2 * BMA * PITCH + (ZSG > 0 ? BN * ZSG * 5 : 20) + 16 * BMA)) / 6 / 64 * 64 > 1024
+             ? 1024
+             : (163840 - 512 - (2 * BMA * PITCH + (ZSG > 0 ? BN * ZSG * 5 : 20) + 16 * BMA)) / 6 / 64 * 64;
+}
+
+// Tile queues of persistent launches: one slot of 256 ints per stream (the
+// per-XCD counters 16 ints apart, the finished-workgroup count at [128]).
+// Zero at load time; every persistent launch leaves its slot zero.
+constexpr int kQueueSlots = 64;
+constexpr int kQueueInts = 256;
+static __device__ __align__(256) int g_tile_queue[kQueueSlots * kQueueInts];
+
 // ZSG > 0: zero points and scales come from an LDS copy of the tile's
 // block; the host launches this only when G <= ZSG (see zs_block_fits).
 //
@@ -1115,8 +1314,21 @@ __device__ __forceinline__ void csr_block(int b, const int (&r0)[kCsrScanChunks]
 // TAIL pairs is computed by the tile of the block before it, as TAIL extra
 // rows of that tile, so its weights are streamed once for both; the short
 // block's own tiles exit.
+//
+// PERSIST: one workgroup per CU (the host sizes the grid to the CU count)
+// takes tiles from queues instead of one tile per workgroup. The tile list
+// is split into 8 equal runs as for the plain grid, one per XCD; workgroup
+// L (on XCD L % 8) draws the next tile of its XCD's run from that run's
+// counter, so the XCD's CUs still work on adjacent tiles at the same time
+// (the row blocks that share a column tile of one expert's weights meet in
+// its L2), and once its own run is exhausted it draws from the other XCDs'
+// runs. The counter for the next tile is incremented when the current tile
+// starts, so its latency hides behind that tile. Compared with one
+// workgroup per tile this saves the retire/launch gap between tiles on a
+// CU and balances the XCDs, whose runs differ in work (tiles of short
+// blocks taken as tails exit at once, and tile heights differ).
 template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST, bool ZSV,
-          int WAVES_PER_EU, int TAIL = 0>
+          int WAVES_PER_EU, int TAIL = 0, bool PERSIST = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU)))
 void w4a8_gemm_kernel(const GemmArgs a) {
   constexpr int BN = NW * WN;
@@ -1124,8 +1336,10 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   constexpr bool ZS_LDS = ZSG > 0;
   constexpr bool ROUTED = RMODE != 0;
   constexpr int BMA = BM + TAIL;   // rows staged: the block and a tail
+  constexpr int CB = compact_blocks(BMA, PITCH, BN, ZSG);
   static_assert(BM % 16 == 0 && WN % 16 == 0 && GS % 64 == 0 && TAIL % 16 == 0, "tile shape");
   static_assert(TAIL == 0 || (ROUTED && BM >= 128 && NW == 8), "tails are taken by routed 8-wave 128-row tiles");
+  static_assert(!PERSIST || (ROUTED && BM >= 64 && CB >= 64), "persistent launches run routed prefill tiles");
 
   __shared__ __attribute__((aligned(16))) int8_t s_x[2 * BMA * PITCH];
   __shared__ __attribute__((aligned(16))) float s_scale[ZS_LDS ? BN * ZSG : 4];
@@ -1138,15 +1352,19 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // ---- tile decode -------------------------------------------------------
+  // ---- tile list -----------------------------------------------------------
   // The grid covers the worst-case block count; the actual count is only
-  // known here. Spread the actual tiles evenly over the 8 XCDs (workgroup L
-  // runs on XCD L % 8), each XCD taking a contiguous run of the tile list.
+  // known here. The actual tiles are split evenly over the 8 XCDs
+  // (workgroup L runs on XCD L % 8), each XCD taking a contiguous run of
+  // the tile list.
   int nblocks;
   int cs_r0[kCsrScanChunks], cs_r1[kCsrScanChunks], cs_incl[kCsrScanChunks];
   if constexpr (ROUTED) {
     // blocks past sorted_len / BM would read past sorted_ids / expert_ids
-    nblocks = min(a.num_post_pad[0] / BM, a.sorted_len / BM);
+    // (a persistent launch's block table holds at most CB; the host bounds
+    // the blocks of such launches by it)
+    nblocks = __builtin_amdgcn_readfirstlane(min(a.num_post_pad[0] / BM, a.sorted_len / BM));
+    if constexpr (PERSIST) nblocks = min(nblocks, CB);
   } else if (a.offsets != nullptr) {
     nblocks = min(csr_scan<BM>(a, cs_r0, cs_r1, cs_incl), a.max_blocks);
   } else {
@@ -1157,59 +1375,239 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   const int span = a.n_tiles * a.R;
   const int tiles = egroups ? nblocks * a.n_tiles : (nblocks + a.R - 1) / a.R * span;
   const int per_xcd = (tiles + 7) >> 3;
-  const int L = blockIdx.x;
-  if ((L >> 3) >= per_xcd) return;
-  const int t = (L & 7) * per_xcd + (L >> 3);
-  if (t >= tiles) return;
-  int b, nt, e, row0 = 0, row1 = 0;
-  if (egroups) {
-    if (!expert_group_tile(t, a.n_tiles, a.R, nblocks, a.expert_ids, a.E, b, nt, e)) return;
-  } else {
-    const int chunk_id = t / span;
-    const int rem = t - chunk_id * span;
-    nt = rem / a.R;
-    b = chunk_id * a.R + group_slot(rem - nt * a.R, nt, a.R);
-    if (b >= nblocks) return;
-    if constexpr (ROUTED) {
-      e = a.expert_ids[b];
-      if (e >= a.E) return;
-    } else if (a.offsets != nullptr) {
-      csr_block<BM>(b, cs_r0, cs_r1, cs_incl, e, row0, row1);
-    } else {
-      e = a.blk_expert[b];
-      row0 = a.blk_row0[b];
-      row1 = a.blk_row1[b];
-    }
-    if (e < 0) return;
-  }
-  int tail = -1;
-  if constexpr (TAIL > 0) {
-    // block b is its expert's short last block, computed by block b - 1's tile
-    if (b > 0 && a.expert_ids[b - 1] == e && short_block<BM, TAIL>(a, b)) return;
-    // this tile computes block b + 1 as its tail
-    if (b + 1 < nblocks && a.expert_ids[b + 1] == e && short_block<BM, TAIL>(a, b + 1)) tail = b + 1;
-  }
 
-  TileCtx c;
-  c.e = e;
-  c.blk = b;
-  c.tail = tail;
-  c.row0 = row0;
-  c.row1 = row1;
-  c.tile_col0 = nt * BN;
-  c.col0 = nt * BN + wave * WN;
-  c.nchunks = (a.G + KCG - 1) / KCG;
-  c.rows = BM;
-  if constexpr (BM < 64) {
-    // Decode tiles request their first weight chunks before the routing
-    // rows are read (the body loads those itself); they decide the
-    // symmetric unpack per group and keep the plain int32 fold -- at these
-    // sizes the weight stream, not the fold, sets the time.
-    gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, false>(a, c, s_x, s_scale, s_zero, s_src,
-                                                                              s_dst, s_xs, s_tw);
+  // Tile t of the list -> its context; false for a tile with no work.
+  auto tile_ctx = [&](int t, TileCtx& c) __attribute__((always_inline)) -> bool {
+    int b, nt, e, row0 = 0, row1 = 0;
+    if (egroups) {
+      if (!expert_group_tile(t, a.n_tiles, a.R, nblocks, a.expert_ids, a.E, b, nt, e)) return false;
+    } else {
+      const int chunk_id = t / span;
+      const int rem = t - chunk_id * span;
+      nt = rem / a.R;
+      b = chunk_id * a.R + group_slot(rem - nt * a.R, nt, a.R);
+      if (b >= nblocks) return false;
+      if constexpr (ROUTED) {
+        e = a.expert_ids[b];
+        if (e >= a.E) return false;
+      } else if (a.offsets != nullptr) {
+        csr_block<BM>(b, cs_r0, cs_r1, cs_incl, e, row0, row1);
+      } else {
+        e = a.blk_expert[b];
+        row0 = a.blk_row0[b];
+        row1 = a.blk_row1[b];
+      }
+      if (e < 0) return false;
+    }
+    int tail = -1;
+    if constexpr (TAIL > 0) {
+      // block b is its expert's short last block, computed by block b - 1's tile
+      if (b > 0 && a.expert_ids[b - 1] == e && short_block<BM, TAIL>(a, b)) return false;
+      // this tile computes block b + 1 as its tail
+      if (b + 1 < nblocks && a.expert_ids[b + 1] == e && short_block<BM, TAIL>(a, b + 1)) tail = b + 1;
+    }
+    // Wave-uniform by construction; said so explicitly because the tile
+    // tables are read with vector loads once the kernel also writes global
+    // memory through atomics, and a descriptor built from a value the
+    // compiler takes as divergent costs a waterfall loop per buffer load.
+    c.e = __builtin_amdgcn_readfirstlane(e);
+    c.blk = __builtin_amdgcn_readfirstlane(b);
+    c.tail = __builtin_amdgcn_readfirstlane(tail);
+    c.row0 = __builtin_amdgcn_readfirstlane(row0);
+    c.row1 = __builtin_amdgcn_readfirstlane(row1);
+    c.tile_col0 = __builtin_amdgcn_readfirstlane(nt * BN);
+    c.col0 = c.tile_col0 + wave * WN;
+    c.nchunks = (a.G + KCG - 1) / KCG;
+    c.rows = BM;
+    return true;
+  };
+  auto run_tile = [&](const TileCtx& c) __attribute__((always_inline)) {
+    if constexpr (BM < 64) {
+      // Decode tiles request their first weight chunks before the routing
+      // rows are read (the body loads those itself); they decide the
+      // symmetric unpack per group and keep the plain int32 fold -- at these
+      // sizes the weight stream, not the fold, sets the time.
+      gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, false>(a, c, s_x, s_scale, s_zero, s_src,
+                                                                                s_dst, s_xs, s_tw);
+    } else {
+      prefill_tile_impl<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, TAIL>(a, c, s_x, s_scale, s_zero, s_src,
+                                                                                   s_dst, s_xs, s_tw);
+    }
+  };
+
+  if constexpr (!PERSIST) {
+    const int L = blockIdx.x;
+    if ((L >> 3) >= per_xcd) return;
+    const int t = (L & 7) * per_xcd + (L >> 3);
+    if (t >= tiles) return;
+    TileCtx c;
+    if (tile_ctx(t, c)) run_tile(c);
   } else {
-    prefill_tile_impl<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, TAIL>(a, c, s_x, s_scale, s_zero, s_src,
-                                                                                 s_dst, s_xs, s_tw);
+    // ---- the launch's row blocks, compacted (LDS) -------------------------
+    // Blocks taken as a tail by the block before them are left out, so every
+    // index of the tile list [0, ncb * n_tiles) is a tile with work; per
+    // compact block: its block (| 0x8000 when it takes the next block as its
+    // tail), its expert, and the compact index of the first block of its
+    // expert's run (a run: consecutive blocks of one expert).
+    constexpr int NT = NW * 64;
+    __shared__ uint16_t s_cb_blk[CB], s_cb_e[CB], s_cb_rs[CB];
+    __shared__ int s_scan[NW];
+    int ncb = 0;
+    for (int b0 = 0; b0 < nblocks; b0 += NT) {
+      const int b = b0 + tid;
+      int e = -1, keep = 0, first = 0, takes = 0;
+      if (b < nblocks) {
+        e = a.expert_ids[b];
+        const int ep = b > 0 ? a.expert_ids[b - 1] : -1;
+        keep = e >= 0 && e < a.E;
+        first = ep != e;
+        if constexpr (TAIL > 0) {
+          const int en = b + 1 < nblocks ? a.expert_ids[b + 1] : -1;
+          if (!first && short_block<BM, TAIL>(a, b)) keep = 0;
+          takes = en == e && short_block<BM, TAIL>(a, b + 1);
+        }
+      }
+      int total;
+      const int pos = ncb + block_scan_add<NW>(keep, s_scan, total) - keep;
+      if (keep) {
+        s_cb_blk[pos] = (uint16_t)(b | (takes ? 0x8000 : 0));
+        s_cb_e[pos] = (uint16_t)e;
+        s_cb_rs[pos] = (uint16_t)(first ? pos : 0xffff);   // run starts; filled in below
+      }
+      ncb += total;
+    }
+    __syncthreads();
+    for (int c0 = 0, carry = -1; c0 < ncb; c0 += NT) {
+      const int cb = c0 + tid;
+      const int v = cb < ncb && s_cb_rs[cb] != 0xffff ? cb : -1;
+      int top;
+      const int rs = max(block_scan_max<NW>(v, s_scan, top), carry);
+      __syncthreads();   // every read of this range's run starts is done
+      if (cb < ncb) s_cb_rs[cb] = (uint16_t)rs;
+      carry = max(carry, top);
+    }
+    __syncthreads();
+    const int ntiles = ncb * a.n_tiles;
+    const int pxcd = (ntiles + 7) >> 3;
+    // tile t -> context, from the compact table: t / n_tiles lies in the
+    // group of its expert's run (groups of R compact blocks from the run's
+    // first), whose tiles take the column tiles in turn, its blocks innermost
+    // in the rotated order of group_slot
+    auto tile_cb = [&](int t, TileCtx& c) __attribute__((always_inline)) {
+      const int R = a.R;
+      const int cb = t / a.n_tiles;
+      const int rs = s_cb_rs[cb];
+      const int g0 = rs + (cb - rs) / R * R;
+      int gs = 1;
+      while (gs < R && g0 + gs < ncb && s_cb_rs[g0 + gs] == rs) ++gs;
+      const int local = t - g0 * a.n_tiles;
+      const int nt = local / gs;
+      const int k = g0 + group_slot(local - nt * gs, nt, gs);
+      const int bi = __builtin_amdgcn_readfirstlane((int)s_cb_blk[k]);
+      c.blk = bi & 0x7fff;
+      c.tail = (bi & 0x8000) ? c.blk + 1 : -1;
+      c.e = __builtin_amdgcn_readfirstlane((int)s_cb_e[k]);
+      c.row0 = c.row1 = 0;
+      c.tile_col0 = __builtin_amdgcn_readfirstlane(nt * BN);
+      c.col0 = c.tile_col0 + wave * WN;
+      c.nchunks = (a.G + KCG - 1) / KCG;
+      c.rows = BM;
+    };
+
+    // ---- tile queues ----------------------------------------------------
+    int* const q = a.queue;
+    const int x = blockIdx.x & 7;
+    // thread 0: the tile of index i drawn from XCD x's counter, or, with
+    // that run exhausted, one drawn from another XCD's run; -1 when every
+    // run is exhausted
+    auto resolve = [&](int i) __attribute__((always_inline)) -> int {
+      const int t0 = x * pxcd;
+      if (i < pxcd && t0 + i < ntiles) return t0 + i;
+      for (int k = 1; k < 8; ++k) {
+        const int y = (x + k) & 7;
+        const int u0 = y * pxcd, u1 = min(u0 + pxcd, ntiles);
+        if (u0 >= u1) continue;
+        const int j = __hip_atomic_fetch_add(q + 16 * y, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (u0 + j < u1) return u0 + j;
+      }
+      return -1;
+    };
+    // (the counter's address passes through a VGPR: with an address known to
+    // be uniform the compiler's atomic optimizer rewrites the add into a
+    // wave-aggregated one whose result it consumes at once, which waits for
+    // every outstanding load and store -- the previous tile's output stores)
+    auto draw = [&]() __attribute__((always_inline)) {
+      __attribute__((address_space(1))) int* qx = (__attribute__((address_space(1))) int*)(q + 16 * x);
+      asm volatile("" : "+v"(qx));
+      return __hip_atomic_fetch_add(qx, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+
+    // ---- tile loop ----------------------------------------------------------
+    // Tile i runs with the next tile's work folded in: its index (requested
+    // when tile i starts) is resolved once tile i's first loads are out;
+    // when tile i's K loop is done every wave decodes it and requests its
+    // routing rows and zero points, which arrive during tile i's epilogue.
+    // Then they go to LDS, and the next tile's row factors are requested,
+    // to be stored just before its own epilogue.
+    constexpr int ZCU = zero_check_units<BN, NT, ZSG>();
+    __shared__ int s_next[2];
+    __shared__ int s_rows[2];
+    if (tid == 0) {
+      s_next[0] = resolve(draw());
+      s_rows[0] = 0;
+    }
+    __syncthreads();
+    int t = __builtin_amdgcn_readfirstlane(s_next[0]);
+    if (t >= 0) {
+      TileCtx c, cn;
+      RowsAhead<ZCU> p;   // the next tile's rows in flight (the first tile's before the loop)
+      tile_cb(t, c);
+      prefill_rows_issue<BM, BN, NT, ZSG, TAIL, ROUTED>(a, c, p);
+      int zok, src, dst;   // this tile's row and symmetric check, settled
+      prefill_rows_settle<BM, BN, NT, ZSG, TAIL, ROUTED>(a, c, p, zok, src, dst);
+      for (int it = 0;; ++it) {
+        const int par = it & 1;
+        int pend = 0;
+        if (tid == 0) pend = draw();
+        float xsv, twv;
+        prefill_rows_place<BM, TAIL, ROUTED, DEBUGP>(a, src, dst, s_src, s_dst, &s_rows[par], xsv, twv);
+        const bool tsym = ZSG > 0 ? __syncthreads_and(zok) != 0 : (__syncthreads(), false);
+        c.rows = __builtin_amdgcn_readfirstlane(s_rows[par]);
+        int tn = -1;
+        auto before = [&]() __attribute__((always_inline)) {
+          if (tid == 0) {
+            s_next[par ^ 1] = resolve(pend);
+            s_rows[par ^ 1] = 0;
+          }
+        };
+        auto after = [&]() __attribute__((always_inline)) {   // (s_next: written before the K loop's barriers)
+          tn = __builtin_amdgcn_readfirstlane(s_next[par ^ 1]);
+          if (tn >= 0) {
+            tile_cb(tn, cn);
+            prefill_rows_issue<BM, BN, NT, ZSG, TAIL, ROUTED>(a, cn, p);
+          }
+        };
+        auto settle = [&]() __attribute__((always_inline)) {
+          if (tn >= 0) prefill_rows_settle<BM, BN, NT, ZSG, TAIL, ROUTED>(a, cn, p, zok, src, dst);
+        };
+        TileHooks<decltype(before), decltype(after), decltype(settle)> hk{before, after, settle, xsv, twv};
+        prefill_run<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, TAIL, decltype(hk)>(
+            a, c, tsym, s_x, s_scale, s_zero, s_src, s_dst, s_xs, s_tw, &hk);
+        __syncthreads();   // every wave is done with the tile's LDS
+        if (tn < 0) break;
+        c = cn;
+      }
+    }
+    // the launch's last workgroup leaves the queues zero for the next launch
+    // on this slot (every workgroup has drawn its last index by now)
+    if (tid == 0) {
+      const int done = __hip_atomic_fetch_add(q + 128, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      if (done == (int)gridDim.x - 1) {
+#pragma unroll
+        for (int y = 0; y < 8; ++y) __hip_atomic_store(q + 16 * y, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(q + 128, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
 }
 
@@ -1231,7 +1629,50 @@ static bool zs_block_fits(const GemmArgs& a, int BN, int ZSG) {
          reinterpret_cast<uintptr_t>(a.wz) % 16 == 0 && (a.ws == nullptr || reinterpret_cast<uintptr_t>(a.ws) % 16 == 0);
 }
 
-template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, int WPE, int TAIL = 0>
+// Persistent launches: the device's CU count and this stream's tile-queue
+// slot (its device address in this file's copy of g_tile_queue). Streams
+// take slots in order of first use; with more than kQueueSlots streams
+// slots are shared, and launches on streams sharing a slot must not run at
+// the same time. A graph captured from a stream keeps that stream's slot.
+static hipError_t persistent_setup(hipStream_t s, int* ncu, int** slot) {
+  constexpr int kDevices = 64;
+  static std::mutex mu;
+  static int* base[kDevices] = {};
+  static int cus[kDevices] = {};
+  static int slot_dev[kQueueSlots];
+  static hipStream_t slot_stream[kQueueSlots];
+  static int n_slots = 0;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (base[dev] == nullptr) {
+    int n = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_tile_queue));
+    if (e != hipSuccess) return e;
+    if (p == nullptr || n <= 0) return hipErrorInvalidValue;
+    cus[dev] = n;
+    base[dev] = static_cast<int*>(p);
+  }
+  int k = 0;
+  while (k < n_slots && k < kQueueSlots && !(slot_dev[k] == dev && slot_stream[k] == s)) ++k;
+  if (k == n_slots || k == kQueueSlots) {
+    k = n_slots % kQueueSlots;
+    slot_dev[k] = dev;
+    slot_stream[k] = s;
+    ++n_slots;
+  }
+  *ncu = cus[dev];
+  *slot = base[dev] + k * kQueueInts;
+  return hipSuccess;
+}
+
+template <int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, int WPE, int TAIL = 0,
+          bool PERSIST = false>
 static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   set_grid(a, max_blocks, NW * WN, R);
   // a column's zero points / scales of one window can be read as one aligned
@@ -1254,16 +1695,42 @@ static hipError_t launch_one(GemmArgs a, int max_blocks, int R, hipStream_t s) {
   // unroll, and (without the LDS zero/scale block) aligned vector runs
   constexpr bool CAN_FAST = BM <= 32;
   constexpr bool RUNS = ZSG == 0;   // vector zero/scale runs apply
-  const dim3 grid(8 * a.per_xcd), block(NW * 64);
-  if (CAN_FAST && a.G % (KCG * RD) == 0 && (ZSG > 0 || a.zs_vec))
-    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, CAN_FAST, RUNS, WPE, TAIL>), grid,
-                       block, 0, s, a);
-  else if (RUNS && a.zs_vec)
-    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, RUNS, WPE, TAIL>), grid,
-                       block, 0, s, a);
-  else
-    hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, false, WPE, TAIL>), grid,
-                       block, 0, s, a);
+  dim3 grid(8 * a.per_xcd), block(NW * 64);
+  // Persistent launches pay off from about 8 tiles a CU (worst-case count;
+  // measured on MI355X: DeepSeek-V3 up/gate M = 4096, ~32 a CU, 1379 ->
+  // 1330 us; Qwen3 M = 2048, ~6 a CU, 108 -> 118 us).
+  if constexpr (PERSIST) {
+    int ncu = 0;
+    const hipError_t e = persistent_setup(s, &ncu, &a.queue);
+    if (e != hipSuccess) return e;
+    // (the compact block table needs the expert-grouped tile order and
+    // room for every block)
+    if (a.egroups && max_blocks <= compact_blocks(BM + TAIL, KCG * GS + 32, NW * WN, ZSG) &&
+        a.total_tiles >= 8 * ncu) {
+      // one workgroup per CU (the tile's LDS allows no second one)
+      grid = dim3(ncu);
+      if (RUNS && a.zs_vec)
+        hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, RUNS, WPE, TAIL, true>),
+                           grid, block, 0, s, a);
+      else
+        hipLaunchKernelGGL(
+            (w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, false, WPE, TAIL, true>), grid,
+            block, 0, s, a);
+      return hipGetLastError();
+    }
+  }
+  {
+    a.queue = nullptr;
+    if (CAN_FAST && a.G % (KCG * RD) == 0 && (ZSG > 0 || a.zs_vec))
+      hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, CAN_FAST, RUNS, WPE, TAIL>),
+                         grid, block, 0, s, a);
+    else if (RUNS && a.zs_vec)
+      hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, RUNS, WPE, TAIL>), grid,
+                         block, 0, s, a);
+    else
+      hipLaunchKernelGGL((w4a8_gemm_kernel<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, false, false, WPE, TAIL>), grid,
+                         block, 0, s, a);
+  }
   return hipGetLastError();
 }
 
@@ -1308,11 +1775,13 @@ hipError_t dispatch_bm(GemmArgs a, const TileConfig& c, int max_blocks, hipStrea
         // 1534 -> 1425 us, every expert at 144 pairs 1782 -> 1443 us.
         if constexpr (RMODE != 0 && GS == 128) {
           if (zs_block_fits(a, 256, 56))
-            return launch_one<128, 32, 8, GS, K256, 2, 56, RMODE, DEBUGP, 2, 16>(a, max_blocks, c.R, s);
+            return launch_one<128, 32, 8, GS, K256, 2, 56, RMODE, DEBUGP, 2, 16, true>(a, max_blocks, c.R, s);
         }
         if (zs_block_fits(a, 256, 64))
-          return launch_one<128, 32, 8, GS, K256, 2, 64, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);
-        return launch_one<128, 32, 8, GS, K256, 2, 0, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);
+          return launch_one<128, 32, 8, GS, K256, 2, 64, RMODE, DEBUGP, 2, 0, RMODE != 0 && GS == 128>(a, max_blocks,
+                                                                                                   c.R, s);
+        return launch_one<128, 32, 8, GS, K256, 2, 0, RMODE, DEBUGP, 2, 0, RMODE != 0 && GS == 128>(a, max_blocks, c.R,
+                                                                                                  s);
       } else
         return launch_one<128, 32, 4, GS, K256, 2, 0, RMODE, DEBUGP, 2>(a, max_blocks, c.R, s);
     default: return hipErrorInvalidValue;

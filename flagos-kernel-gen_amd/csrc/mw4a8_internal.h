@@ -44,6 +44,10 @@ struct GemmArgs {
   // launch geometry (see grid_for)
   int n_tiles, R, total_tiles, per_xcd;
   int egroups;                // routed 64/128-row tiles in expert groups (expert_group_tile)
+  // persistent launches: this launch's tile queues (one counter per XCD,
+  // 16 ints apart, and the count of finished workgroups at [128]); all zero
+  // when the launch starts, and left zero by its last workgroup
+  int* queue;
 };
 
 // Position of block slot i among the gs blocks that share column tile nt in
@@ -55,7 +59,7 @@ struct GemmArgs {
 // the same engines. The order is rotated by the digit sum of nt in base gs
 // (a generalised Thue-Morse sequence), which spreads each block over the
 // positions mod 4 (for gs = 2 and 4: evenly over every 4 column tiles).
-__host__ __device__ inline int group_slot(int i, int nt, int gs) {
+__host__ __device__ __forceinline__ int group_slot(int i, int nt, int gs) {
   if (gs <= 1) return i;
   int r = 0;
   for (int v = nt; v > 0; v /= gs) r += v % gs;
@@ -77,7 +81,7 @@ __host__ __device__ inline int group_slot(int i, int nt, int gs) {
 // block t / n_tiles, so every block of the group is checked to belong to e
 // -- a tile never computes a block with another expert's weights (its tiles
 // may then be skipped; the C ABI requires the ascending order).
-__host__ __device__ inline bool expert_group_tile(int t, int n_tiles, int R, int nblocks, const int32_t* expert_ids,
+__host__ __device__ __forceinline__ bool expert_group_tile(int t, int n_tiles, int R, int nblocks, const int32_t* expert_ids,
                                                   int E, int& b, int& nt, int& e) {
   const int bb = t / n_tiles;
   e = expert_ids[bb];
@@ -103,13 +107,13 @@ __host__ __device__ inline bool expert_group_tile(int t, int n_tiles, int R, int
 // the last one -- loaded by a partial last K-chunk, never computed -- read
 // the last group again, so the offset stays inside the column: the buffer
 // range check does not cover scalar offsets.
-__host__ __device__ inline int w_group_soffset(int gg, int G, int GS) { return (gg < G ? gg : G - 1) * (GS / 2); }
+__host__ __device__ __forceinline__ int w_group_soffset(int gg, int G, int GS) { return (gg < G ? gg : G - 1) * (GS / 2); }
 
 // Vector byte offset of a lane's weight pieces within one expert's
 // [N, K/2] slice: column col, K slot kb (0..3) of the MFMA operand, which
 // covers bytes kb * GS / 8 .. + GS / 8 of each group (16-byte pieces, or one
 // 8-byte piece at group size 64).
-__host__ __device__ inline uint32_t w_lane_offset(int col, uint32_t khalf, int kb, int GS) {
+__host__ __device__ __forceinline__ uint32_t w_lane_offset(int col, uint32_t khalf, int kb, int GS) {
   return (uint32_t)col * khalf + (uint32_t)(kb * (GS / 8));
 }
 

@@ -77,3 +77,35 @@ def test_debug_kernels_are_recognised():
     assert debug and all(ks[n]["file"].startswith("gemm_debug") for n in debug)
     assert not any(_is_debug(n) for n in ks if ks[n]["file"] in ("gemm_routed.resources.txt",
                                                                   "gemm_csr.resources.txt"))
+
+
+LLVM_BIN = "/opt/rocm/llvm/bin"
+
+
+def _calls_in_object(obj, tmp):
+    """Number of s_swappc_b64 (function calls) in the gfx950 code object of
+    one built object file (its .hip_fatbin section, unbundled). Long branches
+    (s_getpc / s_setpc) are not calls and are not counted."""
+    import subprocess
+    base = os.path.join(tmp, os.path.basename(obj))
+    subprocess.run([f"{LLVM_BIN}/llvm-objcopy", f"--dump-section=.hip_fatbin={base}.fatbin", obj], check=True)
+    subprocess.run([f"{LLVM_BIN}/clang-offload-bundler", "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950",
+                    f"--input={base}.fatbin", f"--output={base}.co", "--unbundle"], check=True)
+    dis = subprocess.run([f"{LLVM_BIN}/llvm-objdump", "-d", f"{base}.co"], check=True, capture_output=True,
+                         text=True).stdout
+    return dis.count("s_swappc_b64")
+
+
+def test_no_kernel_calls_a_function(tmp_path):
+    """Every tile body is inlined into its kernel. A tile body the compiler
+    left as a called function (kernel arguments through scratch, its barriers
+    and LDS in the callee) hung the GPU; the lambdas on the tile path are
+    always_inline, and this checks the code objects for any call."""
+    objs = sorted(glob.glob(os.path.join(OBJ_DIR, "gemm_*.o")))
+    if not objs or not os.path.exists(f"{LLVM_BIN}/llvm-objdump"):
+        pytest.skip("library not built or ROCm LLVM tools absent")
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=min(len(objs), 6)) as ex:
+        calls = dict(zip(objs, ex.map(lambda o: _calls_in_object(o, str(tmp_path)), objs)))
+    bad = {os.path.basename(o): n for o, n in calls.items() if n}
+    assert not bad, f"function calls in GEMM code objects: {bad}"
