@@ -256,6 +256,22 @@ __device__ __forceinline__ void row_scales(const GemmArgs& a, int src, int dst, 
   if constexpr (ROUTED) twv = a.tw ? a.tw[dst] : 1.f;
 }
 
+// Routed decode tiles: the sorted_ids entries a thread needs, requested by
+// the kernel entry together with the tile's expert and the block count --
+// its own row's (own, threads < BM) and those of the rows of its XU
+// activation staging units (unit[j] for unit threadIdx.x + j * threads).
+template <int XU>
+struct DecodeSlots {
+  int own;
+  int unit[XU];
+};
+
+// Staging units per thread of a BMX-row tile body (16-byte units of the
+// activation chunk over the workgroup's threads).
+__host__ __device__ constexpr int staging_units(int BMX, int KCG, int GS, int NW) {
+  return (BMX * (KCG * GS / 16) + NW * 64 - 1) / (NW * 64);
+}
+
 // Work a persistent launch fits into a tile body (see the persistent
 // kernel): before_barrier() runs once the body has requested its first
 // chunk's loads (before the body's first barrier), before_epilogue() once
@@ -300,10 +316,10 @@ struct NoHooks {
 //     join, and waited there for every outstanding load, which serialized
 //     the prefetch with the compute.
 template <int BMX, int BM, int WN, int NW, int GS, int KCG, int RD, int ZSG, int RMODE, bool DEBUGP, bool FAST,
-          bool ZSV, bool SYMT, int BMA = BM, class Hooks = NoHooks>
+          bool ZSV, bool SYMT, int BMA = BM, class Hooks = NoHooks, class Pre = std::nullptr_t>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, int8_t* s_x, float* s_scale,
                                           int8_t* s_zero, int* s_src, int* s_dst, float* s_xs, float* s_tw,
-                                          Hooks* hk = nullptr) {
+                                          Hooks* hk = nullptr, const Pre* pre = nullptr) {
   constexpr int NT = NW * 64;
   constexpr int MB = BMX / 16;        // 16-row blocks computed
   constexpr int NB = WN / 16;         // 16-column blocks per wave
@@ -334,9 +350,22 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // Decode tiles (XDEEP, defined below with the activation ring) read their
   // routing rows here, before any weight load: loads complete in issue order,
   // so waiting for these rows never waits for the weights requested next.
+  // PRE: routed decode tiles whose slots the kernel entry has requested
+  // (DecodeSlots): no load here, and the activation offsets come from the
+  // thread's own slots rather than from LDS, so the first activation chunk
+  // is requested with the first weights instead of after a barrier.
+  constexpr bool PRE = !std::is_same<Pre, std::nullptr_t>::value;
   int r_src = -1, r_dst = -1;
   if constexpr (BM < 64) {
-    if (tid < BM) row_source<BM, ROUTED>(a, c, tid, r_src, r_dst);
+    if constexpr (PRE) {
+      static_assert(ROUTED && BM < 64, "preloaded slots are for routed decode tiles");
+      if (tid < BM && pre->own >= 0 && pre->own < a.num_pairs) {
+        r_src = pre->own / a.topk;
+        r_dst = pre->own;
+      }
+    } else {
+      if (tid < BM) row_source<BM, ROUTED>(a, c, tid, r_src, r_dst);
+    }
   }
 
   // ---- buffer descriptors (one expert's slice for the weights) ------------
@@ -387,7 +416,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       const int q = u / UPR;
       const int cu = u - q * UPR;
       const int row = row_of_group<UPR>(q);
-      const int src = s_src[row];
+      int src;
+      if constexpr (PRE) {
+        static_assert(XSURPLUS == 0, "decode staging units divide evenly");
+        const int sid = pre->unit[j];
+        src = sid >= 0 && sid < a.num_pairs ? sid / a.topk : -1;
+      } else {
+        src = s_src[row];
+      }
       x_off[j] = src >= 0 ? (uint32_t)(src * a.ldx) + (uint32_t)(cu * 16) : kOOB;
       x_lds[j] = row * PITCH + unit_pos<GS>(cu);
     }
@@ -527,10 +563,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // kMagic = 0x4B400000 instead of 0, so the int32 result M + P (|P| <= 2^22
   // for every group size here) read as a float is exactly 12582912 + P. One
   // FMA then folds (12582912 + P) * s; the 12582912 * s of the groups is
-  // summed per column (bias) and subtracted from the accumulators every RD
-  // chunks (rebase), which keeps their magnitude, and the extra rounding,
-  // small. Only symmetric tiles with an LDS zero/scale block (SYMT: scales
-  // / 16, so a small bias) take this path; every other tile and kernel
+  // summed per column (bias) and subtracted from the accumulators every
+  // 2 * RD chunks and once after the loop (rebase), which keeps their
+  // magnitude, and the extra rounding, small: with scales / 16 the bias of
+  // 8 groups at group size 128 stays below ~2^17, an ulp of 2^-6 per fold,
+  // far inside the bf16 rounding of the output. Only symmetric tiles with an
+  // LDS zero/scale block (SYMT) take this path; every other tile and kernel
   // keeps the plain int32 chain and a convert.
   bool tile_sym = false;   // decode tiles: every zero point of the tile is 8 (set in the prologue)
   float bias[NB];
@@ -715,6 +753,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         load_w(d, ring[d]);
       }
     }
+    if constexpr (PRE) {
+      init_x();
+#pragma unroll
+      for (int d = 0; d < RD - 1; ++d)
+        if (d < c.nchunks) load_x(d, d);
+    }
     if (tid < BM) {
       s_src[tid] = r_src;
       s_dst[tid] = r_dst;
@@ -732,10 +776,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       }
     }
     tile_sym = __syncthreads_and(zok) != 0;
-    init_x();
+    if constexpr (!PRE) {
+      init_x();
 #pragma unroll
-    for (int d = 0; d < RD - 1; ++d)
-      if (d < c.nchunks) load_x(d, d);
+      for (int d = 0; d < RD - 1; ++d)
+        if (d < c.nchunks) load_x(d, d);
+    }
   } else {
     if constexpr (!ZS_LDS && ZSV) load_zs(0, zs_next);
     load_x(0, 0);
@@ -818,14 +864,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       for (; ch + RD <= c.nchunks; ch += RD) {
 #pragma unroll
         for (int d = 0; d < RD; ++d) interval(ch + d, d, late_tag);
-        rebase();
+        if (ch & RD) rebase();   // every second ring turn (see rebase)
       }
       if (ch < c.nchunks) {
 #pragma unroll
         for (int d = 0; d < RD; ++d)
           if (ch + d < c.nchunks) interval(ch + d, d, late_tag);
-        rebase();
       }
+      rebase();
     };
     if (((tid >> 6) >> 1) & 1) {
       // one more chunk in flight: A(1) in registers, W(RD - 1) in the ring
@@ -899,14 +945,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     for (; ch + RD <= c.nchunks; ch += RD) {
 #pragma unroll
       for (int d = 0; d < RD; ++d) step(ch + d, d);
-      rebase();
+      if (ch & RD) rebase();   // every second ring turn (see rebase)
     }
     if (!FAST && ch < c.nchunks) {
 #pragma unroll
       for (int d = 0; d < RD; ++d)
         if (ch + d < c.nchunks) step(ch + d, d);
-      rebase();
     }
+    rebase();
   }
 
   if constexpr (Hooks::kActive) {
@@ -1357,9 +1403,12 @@ void w4a8_gemm_kernel(const GemmArgs a) {
   // known here. The actual tiles are split evenly over the 8 XCDs
   // (workgroup L runs on XCD L % 8), each XCD taking a contiguous run of
   // the tile list.
-  int nblocks;
+  constexpr bool DECODE_SLOTS = !PERSIST && ROUTED && BM < 64;   // see the routed decode path below
+  int nblocks = 0;
   int cs_r0[kCsrScanChunks], cs_r1[kCsrScanChunks], cs_incl[kCsrScanChunks];
-  if constexpr (ROUTED) {
+  if constexpr (DECODE_SLOTS) {
+    // (read there, after the tile's other loads are out)
+  } else if constexpr (ROUTED) {
     // blocks past sorted_len / BM would read past sorted_ids / expert_ids
     // (a persistent launch's block table holds at most CB; the host bounds
     // the blocks of such launches by it)
@@ -1435,7 +1484,41 @@ void w4a8_gemm_kernel(const GemmArgs a) {
     }
   };
 
-  if constexpr (!PERSIST) {
+  if constexpr (DECODE_SLOTS) {
+    // Routed decode tiles: tile L of the host's worst-case list (tiles past
+    // the actual count exit), so that the tile's block -- and with it its
+    // expert, its slots and the block count -- is known without a load, and
+    // those loads go out together: the weights then follow the expert and the
+    // activations the slots one round trip later (instead of the block count,
+    // the expert, the slots and, after a barrier, the activations one after
+    // the other). Decode blocks share no weights, so the tile order needs no
+    // L2 grouping. The reads stay below the routing buffers' extent
+    // (max_blocks <= sorted_len / BM; the clamp keeps a grid past it in bounds).
+    constexpr int XU = staging_units(BM, KCG, GS, NW);
+    constexpr int UPR = KCG * GS / 16;
+    const int L = blockIdx.x;
+    const int bt = L / a.n_tiles, nt = L - bt * a.n_tiles;
+    const int bs = min(bt, a.sorted_len / BM - 1);
+    DecodeSlots<XU> pre;
+    pre.own = tid < BM ? a.sorted_ids[bs * BM + tid] : -1;
+#pragma unroll
+    for (int j = 0; j < XU; ++j) pre.unit[j] = a.sorted_ids[bs * BM + row_of_group<UPR>((tid + j * NW * 64) / UPR)];
+    const int np = a.num_post_pad[0];
+    const int e = __builtin_amdgcn_readfirstlane(a.expert_ids[bs]);
+    nblocks = __builtin_amdgcn_readfirstlane(min(np / BM, a.sorted_len / BM));
+    if (bt >= nblocks || e < 0 || e >= a.E) return;
+    TileCtx c;
+    c.e = e;
+    c.blk = bt;
+    c.tail = -1;
+    c.row0 = c.row1 = 0;
+    c.tile_col0 = nt * BN;
+    c.col0 = c.tile_col0 + wave * WN;
+    c.nchunks = (a.G + KCG - 1) / KCG;
+    c.rows = BM;
+    gemm_body<BM, BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, false, BM, NoHooks, DecodeSlots<XU>>(
+        a, c, s_x, s_scale, s_zero, s_src, s_dst, s_xs, s_tw, nullptr, &pre);
+  } else if constexpr (!PERSIST) {
     const int L = blockIdx.x;
     if ((L >> 3) >= per_xcd) return;
     const int t = (L & 7) * per_xcd + (L >> 3);
