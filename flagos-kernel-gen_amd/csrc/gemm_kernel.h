@@ -280,8 +280,9 @@ __host__ __device__ constexpr int staging_units(int BMX, int KCG, int GS, int NW
 // waiting for a load issued before the output stores, whose number varies
 // by row, waits for all of them), and the row factors ep_xs / ep_tw
 // (activation scale, routing weight of row threadIdx.x) go to LDS just
-// before the epilogue, their loads having run during the K loop. A plain
-// launch has no hooks.
+// before the epilogue, their loads having run during the K loop. With an
+// LDS zero/scale block, the persistent kernel has stored the tile's block
+// before the body starts. A plain launch has no hooks.
 struct NoHooks {
   static constexpr bool kActive = false;
   float ep_xs = 0.f, ep_tw = 1.f;
@@ -439,7 +440,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   const int s_units = BN * a.G / 4;
   const int z_units = BN * a.G / 16;
   u32x4 sq[SU], zq[ZU];
-  if constexpr (ZS_LDS) {
+  // PZS: a persistent launch loaded this tile's zero/scale block during the
+  // previous tile's epilogue and has stored it to LDS before the body
+  constexpr bool PZS = ZS_LDS && Hooks::kActive;
+  if constexpr (PZS) {
+    // (stored by the persistent kernel)
+  } else if constexpr (ZS_LDS) {
     const uint32_t zbase = (uint32_t)(c.tile_col0 * a.G);
 #pragma unroll
     for (int j = 0; j < SU; ++j) {
@@ -789,7 +795,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     for (int d = 0; d < RD - 1; ++d) load_w(min(d, last_chunk), ring[d]);
     if constexpr (Hooks::kActive) hk->before_barrier();
   }
-  if constexpr (ZS_LDS) {
+  if constexpr (ZS_LDS && !PZS) {
     // visible to all waves after the first barrier of the loop; a symmetric
     // tile stores its scales / 16 for the symmetric unpack (see compute)
 #pragma unroll
@@ -1057,10 +1063,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
 // thread's sorted_ids entry (routed tiles; row tid of the block, or of the
 // tail for tid >= BM) and its share of the tile's [BN x G] zero-point block
 // for the symmetric check (tiles with an LDS zero/scale block).
-template <int ZCU>
+template <int ZCU, int SCU = 1>
 struct RowsAhead {
   int sid;
   u32x4 zq[ZCU];
+  u32x4 sq[SCU];   // persistent launches: the tile's scale block share
 };
 
 template <int BN, int NT, int ZSG>
@@ -1068,9 +1075,14 @@ __host__ __device__ constexpr int zero_check_units() {
   return ZSG > 0 ? (BN * ZSG / 16 + NT - 1) / NT : 1;
 }
 
-template <int BM, int BN, int NT, int ZSG, int TAIL, bool ROUTED>
+template <int BN, int NT, int ZSG>
+__host__ __device__ constexpr int scale_units() {
+  return ZSG > 0 ? (BN * ZSG / 4 + NT - 1) / NT : 1;
+}
+
+template <int BM, int BN, int NT, int ZSG, int TAIL, bool ROUTED, bool DEBUGP = false, int SCU = 1>
 __device__ __forceinline__ void prefill_rows_issue(const GemmArgs& a, const TileCtx& c,
-                                                   RowsAhead<zero_check_units<BN, NT, ZSG>()>& p) {
+                                                   RowsAhead<zero_check_units<BN, NT, ZSG>(), SCU>& p) {
   constexpr int ZCU = zero_check_units<BN, NT, ZSG>();
   const int tid = opaque_tid();
   p.sid = -1;
@@ -1090,12 +1102,33 @@ __device__ __forceinline__ void prefill_rows_issue(const GemmArgs& a, const Tile
   }
 }
 
+// This thread's share of a tile's scale block, loaded ahead (persistent
+// launches: during the previous tile's epilogue).
+template <int BN, int NT, int ZSG, bool DEBUGP, int SCU>
+__device__ __forceinline__ void prefill_scales_issue(const GemmArgs& a, const TileCtx& c,
+                                                     RowsAhead<zero_check_units<BN, NT, ZSG>(), SCU>& p) {
+  static_assert(SCU == scale_units<BN, NT, ZSG>(), "scale block share");
+  const int tid = opaque_tid();
+  // the reference-layout debug export passes no scales (read as zero)
+  const __amdgpu_buffer_rsrc_t sr =
+      (DEBUGP && a.ws == nullptr) ? make_rsrc(a.wz, 0u)
+                                  : make_rsrc(a.ws + (int64_t)c.e * a.N * a.G, (uint32_t)(a.N * a.G) * 4u);
+  const int s_units = BN * a.G / 4;
+#pragma unroll
+  for (int j = 0; j < SCU; ++j) {
+    const int u = tid + j * NT;
+    p.sq[j] = u32x4{0u, 0u, 0u, 0u};
+    if (u < s_units)
+      p.sq[j] = __builtin_amdgcn_raw_buffer_load_b128(sr, (uint32_t)(c.tile_col0 * a.G) * 4u + u * 16u, 0, 0);
+  }
+}
+
 // This thread's row of the tile (src: activation row, dst: output row,
 // -1 for padding) from its sorted_ids entry, and whether its share of the
 // zero-point block is all 8 (columns past N read zero: not symmetric).
-template <int BM, int BN, int NT, int ZSG, int TAIL, bool ROUTED>
+template <int BM, int BN, int NT, int ZSG, int TAIL, bool ROUTED, int SCU = 1>
 __device__ __forceinline__ void prefill_rows_settle(const GemmArgs& a, const TileCtx& c,
-                                                    const RowsAhead<zero_check_units<BN, NT, ZSG>()>& p, int& zok,
+                                                    const RowsAhead<zero_check_units<BN, NT, ZSG>(), SCU>& p, int& zok,
                                                     int& src, int& dst) {
   constexpr int ZCU = zero_check_units<BN, NT, ZSG>();
   const int tid = opaque_tid();
@@ -1643,11 +1676,15 @@ void w4a8_gemm_kernel(const GemmArgs a) {
     int t = __builtin_amdgcn_readfirstlane(s_next[0]);
     if (t >= 0) {
       TileCtx c, cn;
-      RowsAhead<ZCU> p;   // the next tile's rows in flight (the first tile's before the loop)
+      // the next tile's rows and zero/scale block in flight (the first
+      // tile's before the loop)
+      constexpr int SCU = scale_units<BN, NT, ZSG>();
+      RowsAhead<ZCU, SCU> p;
       tile_cb(t, c);
-      prefill_rows_issue<BM, BN, NT, ZSG, TAIL, ROUTED>(a, c, p);
+      prefill_rows_issue<BM, BN, NT, ZSG, TAIL, ROUTED, DEBUGP, SCU>(a, c, p);
+      if constexpr (ZSG > 0) prefill_scales_issue<BN, NT, ZSG, DEBUGP, SCU>(a, c, p);
       int zok, src, dst;   // this tile's row and symmetric check, settled
-      prefill_rows_settle<BM, BN, NT, ZSG, TAIL, ROUTED>(a, c, p, zok, src, dst);
+      prefill_rows_settle<BM, BN, NT, ZSG, TAIL, ROUTED, SCU>(a, c, p, zok, src, dst);
       for (int it = 0;; ++it) {
         const int par = it & 1;
         int pend = 0;
@@ -1656,6 +1693,32 @@ void w4a8_gemm_kernel(const GemmArgs a) {
         prefill_rows_place<BM, TAIL, ROUTED, DEBUGP>(a, src, dst, s_src, s_dst, &s_rows[par], xsv, twv);
         const bool tsym = ZSG > 0 ? __syncthreads_and(zok) != 0 : (__syncthreads(), false);
         c.rows = __builtin_amdgcn_readfirstlane(s_rows[par]);
+        if constexpr (ZSG > 0) {
+          // the tile's zero/scale block (loaded during the previous tile's
+          // epilogue) into LDS -- free since the barrier that ended that tile;
+          // visible to the body after its first barrier. A symmetric tile
+          // stores its scales / 16 and no zero points (see gemm_body).
+          const int s_units = BN * a.G / 4, z_units = BN * a.G / 16;
+#pragma unroll
+          for (int j = 0; j < SCU; ++j) {
+            const int u = tid + j * NT;
+            if (u < s_units) {
+              u32x4 v = p.sq[j];
+              if (tsym) {
+                v.x = __float_as_uint(__uint_as_float(v.x) * 0.0625f);
+                v.y = __float_as_uint(__uint_as_float(v.y) * 0.0625f);
+                v.z = __float_as_uint(__uint_as_float(v.z) * 0.0625f);
+                v.w = __float_as_uint(__uint_as_float(v.w) * 0.0625f);
+              }
+              *reinterpret_cast<u32x4*>(s_scale + 4 * u) = v;
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < ZCU; ++j) {
+            const int u = tid + j * NT;
+            if (!tsym && u < z_units) *reinterpret_cast<u32x4*>(s_zero + 16 * u) = p.zq[j];
+          }
+        }
         int tn = -1;
         auto before = [&]() __attribute__((always_inline)) {
           if (tid == 0) {
@@ -1667,11 +1730,27 @@ void w4a8_gemm_kernel(const GemmArgs a) {
           tn = __builtin_amdgcn_readfirstlane(s_next[par ^ 1]);
           if (tn >= 0) {
             tile_cb(tn, cn);
-            prefill_rows_issue<BM, BN, NT, ZSG, TAIL, ROUTED>(a, cn, p);
+            prefill_rows_issue<BM, BN, NT, ZSG, TAIL, ROUTED, DEBUGP, SCU>(a, cn, p);
+          } else {
+            // (defined on both paths, so that nothing of the previous tile's
+            // loads has to stay live through this tile's K loop)
+            p.sid = -1;
+#pragma unroll
+            for (int j = 0; j < ZCU; ++j) p.zq[j] = u32x4{0u, 0u, 0u, 0u};
           }
         };
         auto settle = [&]() __attribute__((always_inline)) {
-          if (tn >= 0) prefill_rows_settle<BM, BN, NT, ZSG, TAIL, ROUTED>(a, cn, p, zok, src, dst);
+          if (tn >= 0) {
+            prefill_rows_settle<BM, BN, NT, ZSG, TAIL, ROUTED, SCU>(a, cn, p, zok, src, dst);
+            // (the scale loads go out here, after the accumulators have left
+            // their registers, rather than with the rows before the epilogue)
+            if constexpr (ZSG > 0) prefill_scales_issue<BN, NT, ZSG, DEBUGP, SCU>(a, cn, p);
+          } else {
+            zok = 1;
+            src = dst = -1;
+#pragma unroll
+            for (int j = 0; j < SCU; ++j) p.sq[j] = u32x4{0u, 0u, 0u, 0u};
+          }
         };
         TileHooks<decltype(before), decltype(after), decltype(settle)> hk{before, after, settle, xsv, twv};
         prefill_run<BM, WN, NW, GS, KCG, RD, ZSG, RMODE, DEBUGP, FAST, ZSV, TAIL, decltype(hk)>(
