@@ -569,6 +569,54 @@ def test_routed_config_points(pkg, dev, name, M):
     assert_close(out.cpu(), ref, N, f"{name} M={M}")
 
 
+def test_persistent_launches_on_concurrent_streams(pkg, dev):
+    """Persistent launches (routed 128-row tiles with at least 8 worst-case
+    tiles a CU: DeepSeek-V3 up/gate at 80 pairs an expert) on three streams at
+    once, twice: each stream draws tiles from its own queue slot, and every
+    launch leaves its slot at zero, so each output equals the same call run
+    alone (bit for bit: a tile's result does not depend on which workgroup
+    computes it)."""
+    wl = pkg.workloads
+    shape = wl.CONFIGS["dsv3_up"]
+    M = 2560
+    print(f"[persistent] dsv3_up M={M} on 3 streams", flush=True)
+    inp = wl.make_routed_inputs(shape, M, device=dev)
+    assert pkg.select_block_m(M * shape.topk, shape.E, shape.N, shape.K, shape.group_size) == 128
+    routes = [(inp.topk_ids, inp.topk_weights)] + [
+        wl.make_routing(M, shape.E, shape.topk, shape.routing, seed=4242 + r, device=dev) for r in range(2)]
+    args = (inp.x_q, inp.x_scale, inp.w_q4, inp.w_scale, inp.w_zero)
+    alone = []
+    for ids, tw in routes:
+        alone.append(pkg.w4a8_fused_moe(*args, ids, tw, group_size=shape.group_size))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=dev) for _ in routes]
+    for rep in range(2):
+        outs = [None] * len(routes)
+        torch.cuda.synchronize()
+        for i, ((ids, tw), s) in enumerate(zip(routes, streams)):
+            with torch.cuda.stream(s):
+                outs[i] = pkg.w4a8_fused_moe(*args, ids, tw, group_size=shape.group_size)
+        torch.cuda.synchronize()
+        for i in range(len(routes)):
+            assert torch.equal(outs[i], alone[i]), f"stream {i}, round {rep}: differs from the call run alone"
+    # and the oracle on a few experts of the first routing
+    ids = routes[0][0].reshape(-1).cpu()
+    tw = routes[0][1].reshape(-1).cpu()
+    order = torch.argsort(ids, stable=True)
+    counts = torch.bincount(ids.long(), minlength=shape.E).tolist()
+    start = 0
+    for e, c in enumerate(counts):
+        pe = order[start:start + c]
+        start += c
+        if c == 0 or e % 64:
+            continue
+        tok = pe // shape.topk
+        ref = task1_ref.expert_rows_ref(inp.x_q.cpu()[tok], inp.x_scale.cpu()[tok], inp.w_q4[e].cpu(),
+                                        inp.w_scale[e].cpu(), inp.w_zero[e].cpu(), shape.group_size,
+                                        row_weight=tw[pe])
+        assert_close(alone[0].cpu()[pe], ref, shape.N, f"expert {e}")
+
+
 # ------------------------------------------------------------------ graph capture
 
 def test_graph_capture_replays(pkg, dev):
