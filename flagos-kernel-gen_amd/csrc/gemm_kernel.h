@@ -1163,12 +1163,16 @@ __device__ __forceinline__ void prefill_rows_place(const GemmArgs& a, int src, i
   const int tid = opaque_tid();
   xsv = 0.f;
   twv = 1.f;
+  // the last row holding data, per wave: one LDS atomic by lane 0 (a
+  // per-thread atomicMax of divergent values compiles to a loop over the
+  // wave's lanes)
+  const uint64_t have = __ballot(tid < BM + TAIL && dst >= 0);
   if (tid < BM + TAIL) {
     if (dst >= 0) row_scales<ROUTED, DEBUGP>(a, src, dst, xsv, twv);
     s_src[tid] = src;
     s_dst[tid] = dst;
-    if (dst >= 0) atomicMax(s_rows, tid + 1);
   }
+  if (have != 0 && (tid & 63) == 0) atomicMax(s_rows, (tid & ~63) + 64 - __clzll(have));
 }
 
 // Body of a 64/128-row tile whose rows are in LDS (c.rows: rows holding
@@ -1668,9 +1672,11 @@ void w4a8_gemm_kernel(const GemmArgs a) {
     constexpr int ZCU = zero_check_units<BN, NT, ZSG>();
     __shared__ int s_next[2];
     __shared__ int s_rows[2];
+    __shared__ int s_nsym[2];   // nonzero: a zero point of the tile is not 8
     if (tid == 0) {
       s_next[0] = resolve(draw());
       s_rows[0] = 0;
+      s_nsym[0] = 0;
     }
     __syncthreads();
     int t = __builtin_amdgcn_readfirstlane(s_next[0]);
@@ -1685,13 +1691,17 @@ void w4a8_gemm_kernel(const GemmArgs a) {
       if constexpr (ZSG > 0) prefill_scales_issue<BN, NT, ZSG, DEBUGP, SCU>(a, c, p);
       int zok, src, dst;   // this tile's row and symmetric check, settled
       prefill_rows_settle<BM, BN, NT, ZSG, TAIL, ROUTED, SCU>(a, c, p, zok, src, dst);
+      if (!zok) s_nsym[0] = 1;   // (published with the rows below)
       for (int it = 0;; ++it) {
         const int par = it & 1;
         int pend = 0;
         if (tid == 0) pend = draw();
         float xsv, twv;
         prefill_rows_place<BM, TAIL, ROUTED, DEBUGP>(a, src, dst, s_src, s_dst, &s_rows[par], xsv, twv);
-        const bool tsym = ZSG > 0 ? __syncthreads_and(zok) != 0 : (__syncthreads(), false);
+        // one barrier publishes the rows, the row count and the symmetric
+        // flag (raised by the previous tile's epilogue, see settle)
+        __syncthreads();
+        const bool tsym = ZSG > 0 && __builtin_amdgcn_readfirstlane(s_nsym[par]) == 0;
         c.rows = __builtin_amdgcn_readfirstlane(s_rows[par]);
         if constexpr (ZSG > 0) {
           // the tile's zero/scale block (loaded during the previous tile's
@@ -1724,6 +1734,7 @@ void w4a8_gemm_kernel(const GemmArgs a) {
           if (tid == 0) {
             s_next[par ^ 1] = resolve(pend);
             s_rows[par ^ 1] = 0;
+            s_nsym[par ^ 1] = 0;
           }
         };
         auto after = [&]() __attribute__((always_inline)) {   // (s_next: written before the K loop's barriers)
@@ -1742,6 +1753,7 @@ void w4a8_gemm_kernel(const GemmArgs a) {
         auto settle = [&]() __attribute__((always_inline)) {
           if (tn >= 0) {
             prefill_rows_settle<BM, BN, NT, ZSG, TAIL, ROUTED, SCU>(a, cn, p, zok, src, dst);
+            if (!zok) s_nsym[par ^ 1] = 1;   // (reset in before; read after the tile's last barrier)
             // (the scale loads go out here, after the accumulators have left
             // their registers, rather than with the rows before the epilogue)
             if constexpr (ZSG > 0) prefill_scales_issue<BN, NT, ZSG, DEBUGP, SCU>(a, cn, p);
