@@ -617,6 +617,40 @@ def test_persistent_launches_on_concurrent_streams(pkg, dev):
         assert_close(alone[0].cpu()[pe], ref, shape.N, f"expert {e}")
 
 
+def test_persistent_mixed_symmetric_tiles(pkg, dev):
+    """A persistent launch whose tiles switch between the symmetric bodies
+    and the general fold: 128 experts at 130 pairs (258 worst-case row
+    blocks in expert groups -- an expert's weights exceed 4 MiB -- times 16
+    column tiles of 256: over 4000 tiles, above the 8-a-CU threshold of a
+    256-CU device), zero points all 8 on the even experts and uint4 on the
+    odd ones, and on expert 2 a single zero point of 7 (its first column tile
+    must take the general fold). A workgroup learns the body of its next tile
+    from a flag the current tile's epilogue raises; a tile taken as symmetric
+    by mistake would ignore its zero points. Every pair row against the
+    oracle."""
+    wl = pkg.workloads
+    E, N, K, gs, per = 128, 4096, 4096, 128, 130
+    M = E * per
+    print(f"[persistent mixed] E={E} pairs={M} N={N} K={K}", flush=True)
+    g = torch.Generator().manual_seed(2024)
+    labels = torch.arange(E, dtype=torch.int32).repeat_interleave(per)
+    ids = labels[torch.randperm(M, generator=g)].reshape(M, 1).contiguous()
+    tw = torch.rand(M, 1, generator=g) + 0.5
+    w_q4, w_scale, w_zero = wl.make_weights(E, N, K, gs, 91, "cpu", "symmetric")
+    w_zero[1::2] = wl.make_weights(E, N, K, gs, 92, "cpu", "uint4")[2][1::2]
+    w_zero[2, 5, 3] = 7
+    x_q, x_scale = wl.make_activations(M, K, 93, "cpu")
+    assert pkg.select_block_m(M, E, N, K, gs) == 128
+    out = pkg.w4a8_fused_moe(*[t.to(dev) for t in (x_q, x_scale, w_q4, w_scale, w_zero, ids, tw)],
+                             group_size=gs).cpu()
+    flat = ids.reshape(-1)
+    for e in range(E):
+        pe = (flat == e).nonzero().reshape(-1)
+        ref = task1_ref.expert_rows_ref(x_q[pe], x_scale[pe], w_q4[e], w_scale[e], w_zero[e], gs,
+                                        row_weight=tw.reshape(-1)[pe])
+        assert_close(out[pe], ref, N, f"expert {e}")
+
+
 # ------------------------------------------------------------------ graph capture
 
 def test_graph_capture_replays(pkg, dev):
