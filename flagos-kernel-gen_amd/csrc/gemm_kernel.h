@@ -985,9 +985,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     // buffers are free now) so that every row leaves as 16-byte stores of
     // its 256 contiguous bytes -- 8 store instructions per wave instead of 64
     // two-byte ones (an MFMA lane holds four rows of one column). Row r's
-    // 16-byte segment s sits at r * 256 + 16 * (s ^ (r % 16)): the four rows
-    // of one ds_write_b16 hit distinct segments, and so do the two rows of a
-    // ds_read_b128 half-wave (opposite parity: disjoint bank halves).
+    // 16-byte segment s sits at r * ROWB + 16 * (s ^ 2 ((r / 4) % 4)): the
+    // four rows of one ds_write_b16 (r / 4 % 4 = the lane's K slot, the rows'
+    // segment pairs XORed with 0, 2, 4, 6) hit 8 distinct segments, and a
+    // ds_read_b128 half-wave reads one row's segments permuted. The XOR term
+    // is the lane's own for every write, so each write's address is a lane
+    // base plus an immediate (a term with the row's low bits cost ~4 VALU a
+    // write).
     constexpr bool TILE_OUT = (BN == 128 || BN == 256) && BM >= 64;
     constexpr int SEG = BN / 8;          // 16-byte segments per tile row
     constexpr int ROWB = BN * 2;         // bytes per tile row
@@ -1010,12 +1014,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
             }
             // rows r and r + 1 of the column converted as one pair
             const uint32_t pk[2] = {bf16x2_rne(v[0], v[1]), bf16x2_rne(v[2], v[3])};
+            // this lane's rows kb * 4 + r of block mb: (row / 4) % 4 = kb
+            uint8_t* const lb = tile + kb * 4 * ROWB + (((cl >> 3) ^ (kb << 1)) << 4) + ((cl & 7) << 1);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int row = mb * 16 + kb * 4 + r;
-              const int off = row * ROWB + (((cl >> 3) ^ (row & (SEG - 1))) << 4) + ((cl & 7) << 1);
-              *reinterpret_cast<uint16_t*>(tile + off) = (uint16_t)(pk[r >> 1] >> (16 * (r & 1)));
-            }
+            for (int r = 0; r < 4; ++r)
+              *reinterpret_cast<uint16_t*>(lb + (mb * 16 + r) * ROWB) = (uint16_t)(pk[r >> 1] >> (16 * (r & 1)));
           }
         __syncthreads();
         if constexpr (Hooks::kActive) hk->before_stores();
@@ -1024,7 +1027,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
         for (int i = 0; i < BMX * SEG / NT; ++i) {
           const int t = tid + i * NT;
           const int row = t / SEG, seg = t % SEG;
-          const u32x4 v = *reinterpret_cast<const u32x4*>(tile + row * ROWB + ((seg ^ (row & (SEG - 1))) << 4));
+          const u32x4 v = *reinterpret_cast<const u32x4*>(tile + row * ROWB + ((seg ^ (((row >> 2) & 3) << 1)) << 4));
           const int dst = s_dst[row];
           const int col = c.tile_col0 + seg * 8;
           if (dst >= 0 && col < a.N) *reinterpret_cast<u32x4*>(a.out + (int64_t)dst * a.ldo + col) = v;
