@@ -590,10 +590,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
   // for every group size here) read as a float is exactly 12582912 + P. One
   // FMA then folds (12582912 + P) * s; the 12582912 * s of the groups is
   // summed per column (bias) and subtracted from the accumulators every
-  // 2 * RD chunks and once after the loop (rebase), which keeps their
+  // 4 * RD chunks and once after the loop (rebase), which keeps their
   // magnitude, and the extra rounding, small: with scales / 16 the bias of
-  // 8 groups at group size 128 stays below ~2^17, an ulp of 2^-6 per fold,
-  // far inside the bf16 rounding of the output. Only symmetric tiles with an
+  // 16 groups at group size 128 stays below ~2^18, an ulp of 2^-5 per fold,
+  // far inside the bf16 rounding of the output. (Every 2 * RD chunks
+  // measured 0.4-0.7 % slower on the 128-row prefill points: the rebase is
+  // 64 subtractions.) Only symmetric tiles with an
   // LDS zero/scale block (SYMT) take this path; every other tile and kernel
   // keeps the plain int32 chain and a convert.
   bool tile_sym = false;   // decode tiles: every zero point of the tile is 8 (set in the prologue)
@@ -890,7 +892,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
       for (; ch + RD <= c.nchunks; ch += RD) {
 #pragma unroll
         for (int d = 0; d < RD; ++d) interval(ch + d, d, late_tag);
-        if (ch & RD) rebase();   // every second ring turn (see rebase)
+        if ((ch & (3 * RD)) == 3 * RD) rebase();   // every fourth ring turn (see rebase)
       }
       if (ch < c.nchunks) {
 #pragma unroll
@@ -971,7 +973,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TileCtx& c, i
     for (; ch + RD <= c.nchunks; ch += RD) {
 #pragma unroll
       for (int d = 0; d < RD; ++d) step(ch + d, d);
-      if (ch & RD) rebase();   // every second ring turn (see rebase)
+      if ((ch & (3 * RD)) == 3 * RD) rebase();   // every fourth ring turn (see rebase)
     }
     if (!FAST && ch < c.nchunks) {
 #pragma unroll
